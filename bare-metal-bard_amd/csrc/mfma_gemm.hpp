@@ -1,0 +1,266 @@
+// fp32 matrix-core GEMM for gfx950: v_mfma_f32_32x32x2_f32.
+//
+// One kernel template serves SGEMM stage 9 (sgemm_tensorcore), the
+// transpose-aware gemm() and batched_gemm() (src/gemm.cu, src/bgemm.cu are the
+// reference's counterparts). Inputs are fp32, each product is an exact fp32
+// product and accumulation is fp32, so the result differs from the sequential
+// fp32 oracle only by summation order (normwise ~1e-7 at K = 4096).
+//
+// MFMA operand layout used (v_mfma_f32_32x32x2_f32, one block):
+//   A operand: lane l supplies A[m = l % 32][kk = l / 32]
+//   B operand: lane l supplies B[kk = l / 32][n = l % 32]
+//   D: lane l holds column n = l % 32, register r holds row
+//      8 * (r / 4) + 4 * (l / 32) + r % 4.
+// A K-chunk of 8 is consumed as 4 MFMAs; MFMA j pairs k = j (lanes 0-31) with
+// k = 4 + j (lanes 32-63). The pairing is a permutation of the 8 k values
+// applied identically to A and B, so the sum is unchanged; it lets a lane
+// fetch its 4 k values of a k-contiguous LDS row with one 128-bit read.
+//
+// LDS layouts (each a direct copy of the operand's global layout, so staging
+// is 128-bit loads and 128-bit stores with no transposition):
+//   A, transA = false: As[m][k] (row stride BK + 4)  -> 128-bit fragment reads
+//   A, transA = true : As[k][m] (row stride BM + 8)  -> 32-bit fragment reads
+//   B, transB = false: Bs[k][n] (row stride BN + 8)  -> 32-bit fragment reads
+//   B, transB = true : Bs[n][k] (row stride BK + 4)  -> 128-bit fragment reads
+// The +4 pad spreads 16 consecutive rows of a 128-bit read over all 64 banks;
+// the +8 pad puts the two half-waves of a 32-bit read (rows 4 apart) in
+// opposite halves of the banks.
+#pragma once
+
+#include "common.hpp"
+
+namespace bmb {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
+struct MfmaTile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_;
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr int NT = WAVES_M * WAVES_N * 64;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FM = WM / 32, FN = WN / 32;
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is whole 32x32 MFMA tiles");
+    static_assert(BK % 8 == 0, "BK is a whole number of 8-k groups");
+};
+
+template <bool TA, bool TB, class Tile>
+struct MfmaLayout {
+    static constexpr int BM = Tile::BM, BN = Tile::BN, BK = Tile::BK, NT = Tile::NT;
+    // A
+    static constexpr int LDA = TA ? BM + 8 : BK + 4;
+    static constexpr int A_ROWS = TA ? BK : BM;  // rows of the LDS A array
+    static constexpr int A_SZ = A_ROWS * LDA;
+    static constexpr int A_CHUNKS = BM * BK / 4;  // float4 chunks per tile
+    static constexpr int A_PER_T = A_CHUNKS / NT;
+    // B
+    static constexpr int LDB = TB ? BK + 4 : BN + 8;
+    static constexpr int B_ROWS = TB ? BN : BK;
+    static constexpr int B_SZ = B_ROWS * LDB;
+    static constexpr int B_CHUNKS = BK * BN / 4;
+    static constexpr int B_PER_T = B_CHUNKS / NT;
+    static_assert(A_CHUNKS % NT == 0 && B_CHUNKS % NT == 0, "staging tiles evenly");
+    static constexpr int STAGE = A_SZ + B_SZ;  // floats per pipeline stage
+    static constexpr size_t SMEM_BYTES = 2 * (size_t)STAGE * sizeof(float);
+};
+
+// Loads one operand chunk (4 floats along the operand's contiguous axis) from
+// global memory, zero filling whatever lies outside [0, rows) x [0, cols).
+// `row` and `col0` index the stored matrix (rows x cols, row-major).
+template <bool VEC>
+__device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols,
+                                             int row, int col0) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row >= rows) return v;
+    const float *p = P + (size_t)row * cols + col0;
+    if (VEC) {
+        if (col0 < cols) v = ld4(p);
+    } else {
+        if (col0 + 0 < cols) v.x = p[0];
+        if (col0 + 1 < cols) v.y = p[1];
+        if (col0 + 2 < cols) v.z = p[2];
+        if (col0 + 3 < cols) v.w = p[3];
+    }
+    return v;
+}
+
+template <bool TA, bool TB, class Tile, bool VEC>
+struct MfmaGemm {
+    using L = MfmaLayout<TA, TB, Tile>;
+    static constexpr int BM = Tile::BM, BN = Tile::BN, BK = Tile::BK, NT = Tile::NT;
+    static constexpr int WM = Tile::WM, WN = Tile::WN, FM = Tile::FM, FN = Tile::FN;
+
+    struct Regs {
+        float4 a[L::A_PER_T];
+        float4 b[L::B_PER_T];
+    };
+
+    // Chunk e of the A tile: which stored row and which 4-column group.
+    __device__ static __forceinline__ void a_chunk(int e, int &r, int &c) {
+        if (TA) { r = e / (BM / 4); c = (e % (BM / 4)) * 4; }  // stored K x M
+        else    { r = e / (BK / 4); c = (e % (BK / 4)) * 4; }  // stored M x K
+    }
+    __device__ static __forceinline__ void b_chunk(int e, int &r, int &c) {
+        if (TB) { r = e / (BK / 4); c = (e % (BK / 4)) * 4; }  // stored N x K
+        else    { r = e / (BN / 4); c = (e % (BN / 4)) * 4; }  // stored K x N
+    }
+
+    __device__ static __forceinline__ void load(Regs &g, const float *A,
+                                                const float *B, int M, int N,
+                                                int K, int m0, int n0, int k0,
+                                                int tid) {
+#pragma unroll
+        for (int i = 0; i < L::A_PER_T; ++i) {
+            int r, c;
+            a_chunk(tid + i * NT, r, c);
+            g.a[i] = TA ? load_chunk<VEC>(A, K, M, k0 + r, m0 + c)
+                        : load_chunk<VEC>(A, M, K, m0 + r, k0 + c);
+        }
+#pragma unroll
+        for (int i = 0; i < L::B_PER_T; ++i) {
+            int r, c;
+            b_chunk(tid + i * NT, r, c);
+            g.b[i] = TB ? load_chunk<VEC>(B, N, K, n0 + r, k0 + c)
+                        : load_chunk<VEC>(B, K, N, k0 + r, n0 + c);
+        }
+    }
+
+    __device__ static __forceinline__ void store(const Regs &g, float *as,
+                                                 float *bs, int tid) {
+#pragma unroll
+        for (int i = 0; i < L::A_PER_T; ++i) {
+            int r, c;
+            a_chunk(tid + i * NT, r, c);
+            st4(as + r * L::LDA + c, g.a[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < L::B_PER_T; ++i) {
+            int r, c;
+            b_chunk(tid + i * NT, r, c);
+            st4(bs + r * L::LDB + c, g.b[i]);
+        }
+    }
+
+    // Fragments of one 8-k group for this lane: fa[fi][j], fb[fn][j].
+    __device__ static __forceinline__ void fragments(const float *as,
+                                                     const float *bs, int g,
+                                                     int wm, int wn, int lane,
+                                                     float (&fa)[FM][4],
+                                                     float (&fb)[FN][4]) {
+        const int l32 = lane & 31, half = lane >> 5;
+        const int kq = g * 8 + half * 4;
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi) {
+            const int m = wm + fi * 32 + l32;
+            if (TA) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) fa[fi][j] = as[(kq + j) * L::LDA + m];
+            } else {
+                const float4 v = ld4(as + m * L::LDA + kq);
+                fa[fi][0] = v.x; fa[fi][1] = v.y; fa[fi][2] = v.z; fa[fi][3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int n = wn + fn * 32 + l32;
+            if (TB) {
+                const float4 v = ld4(bs + n * L::LDB + kq);
+                fb[fn][0] = v.x; fb[fn][1] = v.y; fb[fn][2] = v.z; fb[fn][3] = v.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) fb[fn][j] = bs[(kq + j) * L::LDB + n];
+            }
+        }
+    }
+
+    // One output tile (m0, n0) of one problem. smem holds two stages.
+    __device__ static __forceinline__ void run(int M, int N, int K, float alpha,
+                                               const float *__restrict__ A,
+                                               const float *__restrict__ B,
+                                               float beta, float *C, int m0,
+                                               int n0, float *smem) {
+        const int tid = threadIdx.x;
+        const int wave = tid >> 6, lane = tid & 63;
+        const int wm = (wave / Tile::WAVES_N) * WM;
+        const int wn = (wave % Tile::WAVES_N) * WN;
+
+        f32x16 acc[FM][FN];
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[fi][fn][r] = 0.0f;
+
+        const int nkt = (K + BK - 1) / BK;
+        Regs g;
+        if (nkt > 0) {
+            load(g, A, B, M, N, K, m0, n0, 0, tid);
+            store(g, smem, smem + L::A_SZ, tid);
+        }
+        __syncthreads();
+
+        for (int kt = 0; kt < nkt; ++kt) {
+            float *stage = smem + (kt & 1) * L::STAGE;
+            const bool more = kt + 1 < nkt;
+            if (more) load(g, A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+
+            const float *as = stage, *bs = stage + L::A_SZ;
+#pragma unroll
+            for (int grp = 0; grp < BK / 8; ++grp) {
+                float fa[FM][4], fb[FN][4];
+                fragments(as, bs, grp, wm, wn, lane, fa, fb);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fi][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                fa[fi][j], fb[fn][j], acc[fi][fn], 0, 0, 0);
+            }
+
+            if (more) {
+                float *next = smem + ((kt + 1) & 1) * L::STAGE;
+                store(g, next, next + L::A_SZ, tid);
+            }
+            __syncthreads();
+        }
+
+        // Epilogue: lanes 0-31 of a register cover 32 consecutive columns, so
+        // each C row segment is one 128-byte coalesced access.
+        const int l32 = lane & 31, half = lane >> 5;
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+                const int col = n0 + wn + fn * 32 + l32;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (row < M) {
+                        float *dst = C + (size_t)row * N + col;
+                        *dst = epilogue(acc[fi][fn][r], alpha, beta, dst);
+                    }
+                }
+            }
+    }
+};
+
+// Grid: x = output tiles (XCD-remapped, grouped), y = batch index.
+template <bool TA, bool TB, class Tile, bool VEC>
+__global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
+    int M, int N, int K, float alpha, const float *__restrict__ A,
+    long long sA, const float *__restrict__ B, long long sB, float beta,
+    float *C, long long sC, int tiles_m, int tiles_n) {
+    extern __shared__ float smem_dyn[];
+    const size_t z = blockIdx.y;
+    int tm, tn;
+    group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    MfmaGemm<TA, TB, Tile, VEC>::run(M, N, K, alpha, A + z * sA, B + z * sB,
+                                     beta, C + z * sC, tm * Tile::BM,
+                                     tn * Tile::BN, smem_dyn);
+}
+
+}  // namespace bmb

@@ -1,0 +1,58 @@
+/*
+ * Fused causal multi-head attention, forward and backward -- C-ABI drop-in for
+ * bare-metal-bard's src/flash.h.
+ *
+ * Buffer shapes (src/flash.h:29-35), all fp32, caller-owned device memory:
+ *   qkv  (B, T, 3C)   fused QKV projection output, [q|k|v] along 3C,
+ *                     head h at column offset h*hs, hs = C / NH
+ *   out  (B, T, C)
+ *   lse  (B, NH, T)   natural-log log-sum-exp of each row's scaled scores
+ *   dqkv (B, T, 3C)   written, not accumulated
+ *   dsum (B, NH, T)   backward scratch: rowsum(dout * out)
+ * scale = 1/sqrt(hs). The T x T score matrix is never materialised. Launches
+ * go to the null stream. Supported head sizes: 32, 64, 128.
+ */
+#ifndef BMB_FLASH_H
+#define BMB_FLASH_H
+
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* src/flash.h:36-37. Runs the default config, then any legal config; if none
+ * fits the head size, prints a message and calls exit(1) like the reference
+ * (src/flash.cu:419-432). */
+void flash_attention_forward(float *out, float *lse, const float *qkv, int B,
+                             int T, int C, int NH);
+
+/* src/flash.h:39-41. Same fallback rule (src/flash.cu:988-1003). */
+void flash_attention_backward(float *dqkv, float *dsum, const float *dout,
+                              const float *qkv, const float *out,
+                              const float *lse, int B, int T, int C, int NH);
+
+/* Tuning harness, src/flash.h:48-53: configs are enumerated and named; the
+ * _cfg entry returns false (launching nothing) for an unknown id, a head size
+ * the config cannot serve, or a shape it cannot run. */
+int flash_num_configs(void);
+const char *flash_config_name(int cfg);
+int flash_default_config(void);
+bool flash_attention_forward_cfg(int cfg, float *out, float *lse,
+                                 const float *qkv, int B, int T, int C, int NH);
+
+/* src/flash.h:56-62 */
+int flash_num_bwd_configs(void);
+const char *flash_bwd_config_name(int cfg);
+int flash_default_bwd_config(void);
+bool flash_attention_backward_cfg(int cfg, float *dqkv, float *dsum,
+                                  const float *dout, const float *qkv,
+                                  const float *out, const float *lse, int B,
+                                  int T, int C, int NH);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,46 @@
+/*
+ * Transpose-aware and batched GEMM -- C-ABI drop-in for bare-metal-bard's
+ * src/gemm.h.
+ *
+ * Row-major throughout (src/gemm.h:4-11):
+ *     C[M,N] = alpha * op(A) @ op(B) + beta * C
+ *     op(A) = A   with A stored M x K (lda = K)   when transA == false
+ *           = A^T with A stored K x M (lda = M)   when transA == true
+ *     op(B) = B   with B stored K x N (ldb = N)   when transB == false
+ *           = B^T with B stored N x K (ldb = K)   when transB == true
+ * Pointers are caller-owned device pointers. beta == 0 means C is write-only.
+ * Computation is fp32 in, fp32 products, fp32 accumulation on MFMA matrix
+ * cores; normwise error against an exact reference is at fp32 rounding level
+ * (held to 1e-4, the reference's bar, tools/test_gemm.cu:107).
+ */
+#ifndef BMB_GEMM_H
+#define BMB_GEMM_H
+
+#include <hip/hip_runtime_api.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
+
+#ifdef __cplusplus
+#define BMB_DEFAULT_STREAM = 0
+extern "C" {
+#else
+#define BMB_DEFAULT_STREAM
+#endif
+
+/* src/gemm.h:17-19 (cudaStream_t becomes hipStream_t; 0 = null stream). */
+void gemm(bool transA, bool transB, int M, int N, int K, float alpha,
+          const float *A, const float *B, float beta, float *C,
+          hipStream_t stream BMB_DEFAULT_STREAM);
+
+/* src/gemm.h:26-29: `batch` independent problems; problem z reads
+ * A + z*strideA, B + z*strideB and updates C + z*strideC. */
+void batched_gemm(bool transA, bool transB, int batch, int M, int N, int K,
+                  float alpha, const float *A, long long strideA,
+                  const float *B, long long strideB, float beta, float *C,
+                  long long strideC, hipStream_t stream BMB_DEFAULT_STREAM);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

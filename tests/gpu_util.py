@@ -1,0 +1,57 @@
+"""Device-memory helpers for the GPU parity tests.
+
+torch is used only to allocate device memory and copy bytes; every
+computation under test goes through the C-ABI of lib/libbmb.so.
+"""
+import numpy as np
+import torch
+
+import bmb
+
+GUARD = 64            # floats of canary on each side of an output buffer
+CANARY = 0x7FA5A5A5   # a quiet-NaN bit pattern no kernel produces
+POISON = 0x7F7F7F7F   # 3.39e38: what the reference test poisons outputs with
+
+
+def dev(a):
+    """Host numpy array -> device float32 tensor (contiguous copy)."""
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def sync(what="kernel"):
+    torch.cuda.synchronize()
+    bmb.check(what)
+
+
+class Guarded:
+    """A device float32 buffer with canary bands on both sides.
+
+    ptr points at the payload (16-byte aligned); ok() checks the bands."""
+
+    def __init__(self, n, fill=None, poison=False):
+        self.n = n
+        self.buf = torch.empty(n + 2 * GUARD, dtype=torch.float32, device="cuda")
+        self.buf.view(torch.int32).fill_(CANARY - (1 << 32) if CANARY >= 1 << 31 else CANARY)
+        payload = self.buf[GUARD:GUARD + n]
+        if fill is not None:
+            payload.copy_(torch.from_numpy(np.ascontiguousarray(fill, dtype=np.float32).reshape(-1)))
+        elif poison:
+            payload.view(torch.int32).fill_(POISON)
+        self.payload = payload
+
+    @property
+    def ptr(self):
+        return self.payload.data_ptr()
+
+    def get(self):
+        return host(self.payload)
+
+    def ok(self):
+        h = host(self.buf.view(torch.int32))
+        c = np.int32(np.uint32(CANARY).view(np.int32))
+        return bool((h[:GUARD] == c).all() and (h[GUARD + self.n:] == c).all())

@@ -1,0 +1,134 @@
+"""SGEMM kernel table on the GPU against the CPU oracle.
+
+Mirrors the verify step of src/bench.cu:259-273 (alpha=0.5, beta=3.0, C
+pre-filled, normwise metric, NaN/Inf fail) with the oracle in place of
+cuBLAS, plus bit-exactness for the fp32 VALU stages, canary bands around C,
+ragged shapes with no fallback, and the beta == 0 write-only contract.
+"""
+import numpy as np
+import pytest
+
+import bmb
+import oracle as O
+from gpu_util import Guarded, dev, sync
+
+pytestmark = pytest.mark.gpu
+
+SEED_A, SEED_B, SEED_C = 0x12345678, 0x9ABCDEF0, 0x0F0F0F0F  # src/bench.cu:226-228
+VALU_IDS = [1, 2, 3, 4, 5, 6, 7, 8]
+MFMA_IDS = [9, 10]
+SHAPES = [  # (M, N, K)
+    (128, 128, 128), (256, 256, 256), (512, 512, 512), (1024, 1024, 1024),
+    (1000, 1000, 1000), (100, 70, 33), (65, 65, 65), (130, 260, 60),
+    (1, 1, 1), (7, 13, 5), (33, 1, 70), (64, 64, 0),
+]
+
+
+def _inputs(M, N, K):
+    A = O.fill_xorshift(M * K, SEED_A).reshape(M, K)
+    B = O.fill_xorshift(K * N, SEED_B).reshape(K, N)
+    C0 = O.fill_xorshift(M * N, SEED_C).reshape(M, N)
+    return A, B, C0
+
+
+def _run(kid, M, N, K, alpha, beta, A, B, C0):
+    dA, dB = dev(A), dev(B)
+    gC = Guarded(M * N, fill=C0)
+    print("sgemm id=%d M=%d N=%d K=%d alpha=%g beta=%g" % (kid, M, N, K, alpha, beta), flush=True)
+    bmb.sgemm(kid, M, N, K, alpha, dA.data_ptr(), dB.data_ptr(), beta, gC.ptr)
+    sync("sgemm id %d" % kid)
+    assert gC.ok(), "canary band around C overwritten"
+    return gC.get().reshape(M, N)
+
+
+def test_table_contents(gpu):
+    ids = [k[0] for k in bmb.kernels()]
+    assert ids == list(range(1, 11))
+    assert bmb.find_kernel(0) is None and bmb.find_kernel(11) is None
+
+
+@pytest.mark.parametrize("kid", VALU_IDS)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%dx%d" % s)
+def test_valu_bit_exact(gpu, kid, shape):
+    """fp32 VALU stages equal the sequential-fmaf oracle bit for bit."""
+    M, N, K = shape
+    A, B, C0 = _inputs(M, N, K)
+    got = _run(kid, M, N, K, 0.5, 3.0, A, B, C0)
+    want = O.gemm_f32seq(0, 0, M, N, K, 0.5, A, B, 3.0, C0, threads=0)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got, want), "max |diff| = %g" % np.abs(got - want).max()
+    ref = O.gemm_f64(0, 0, M, N, K, 0.5, A, B, 3.0, C0)
+    err, bad = O.normwise(got, ref)
+    assert bad == 0 and err < bmb.find_kernel(kid)["tol"]
+
+
+@pytest.mark.parametrize("kid", MFMA_IDS)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%dx%d" % s)
+def test_mfma_within_tol(gpu, kid, shape):
+    M, N, K = shape
+    A, B, C0 = _inputs(M, N, K)
+    got = _run(kid, M, N, K, 0.5, 3.0, A, B, C0)
+    ref = O.gemm_f64(0, 0, M, N, K, 0.5, A, B, 3.0, C0)
+    err, bad = O.normwise(got, ref)
+    print("id %d %s normwise %.3e" % (kid, shape, err))
+    assert bad == 0
+    assert err < bmb.find_kernel(kid)["tol"]
+    if kid == 9:  # fp32 products: only the summation order differs
+        assert err < 2e-6
+
+
+@pytest.mark.parametrize("kid", [8, 9, 10])
+@pytest.mark.parametrize("n", [4096, 4097])
+def test_large_sampled_rows(gpu, kid, n):
+    """BASELINE sizes; rows are independent, so a row sample of the oracle
+    checks the full-size launch (incl. the ragged 4097 edge rows)."""
+    M = N = K = n
+    A, B, C0 = _inputs(M, N, K)
+    got = _run(kid, M, N, K, 1.0, 0.5, A, B, C0)
+    rows = np.unique(np.r_[0, 1, 127, 128, 255, 256, 1000, n // 2, n - 129, n - 2, n - 1,
+                           np.random.default_rng(7).integers(0, n, 8)])
+    As = A[rows]
+    ref = O.gemm_f64(0, 0, len(rows), N, K, 1.0, As, B, 0.5, C0[rows])
+    err, bad = O.normwise(got[rows], ref)
+    assert bad == 0 and err < bmb.find_kernel(kid)["tol"]
+    if kid == 8:
+        want = O.gemm_f32seq(0, 0, len(rows), N, K, 1.0, As, B, 0.5, C0[rows], threads=0)
+        assert np.array_equal(got[rows], want)
+
+
+@pytest.mark.parametrize("kid", VALU_IDS + MFMA_IDS)
+def test_beta_zero_is_write_only(gpu, kid):
+    """beta == 0 never reads C: a NaN-filled C gives alpha*A@B."""
+    M, N, K = 130, 200, 48
+    A, B, _ = _inputs(M, N, K)
+    C0 = np.full((M, N), np.nan, np.float32)
+    got = _run(kid, M, N, K, 1.25, 0.0, A, B, C0)
+    assert np.isfinite(got).all()
+    ref = O.gemm_f64(0, 0, M, N, K, 1.25, A, B, 0.0, None)
+    err, _ = O.normwise(got, ref)
+    assert err < bmb.find_kernel(kid)["tol"]
+    if kid in VALU_IDS:
+        want = O.gemm_f32seq(0, 0, M, N, K, 1.25, A, B, 0.0, None)
+        assert np.array_equal(got, want)
+
+
+def test_misaligned_pointers(gpu):
+    """Pointers off 16-byte alignment take the scalar-load paths."""
+    M, N, K = 96, 72, 40
+    A, B, C0 = _inputs(M, N, K)
+    import torch
+    dA = torch.zeros(M * K + 1, dtype=torch.float32, device="cuda")
+    dB = torch.zeros(K * N + 1, dtype=torch.float32, device="cuda")
+    dC = torch.zeros(M * N + 1, dtype=torch.float32, device="cuda")
+    dA[1:].copy_(torch.from_numpy(A.reshape(-1)))
+    dB[1:].copy_(torch.from_numpy(B.reshape(-1)))
+    for kid in VALU_IDS + MFMA_IDS:
+        dC[1:].copy_(torch.from_numpy(C0.reshape(-1)))
+        bmb.sgemm(kid, M, N, K, 0.5, dA[1:].data_ptr(), dB[1:].data_ptr(), 3.0, dC[1:].data_ptr())
+        sync()
+        got = dC[1:].cpu().numpy().reshape(M, N)
+        ref = O.gemm_f64(0, 0, M, N, K, 0.5, A, B, 3.0, C0)
+        err, bad = O.normwise(got, ref)
+        assert bad == 0 and err < bmb.find_kernel(kid)["tol"], kid
+        if kid in VALU_IDS:
+            assert np.array_equal(got, O.gemm_f32seq(0, 0, M, N, K, 0.5, A, B, 3.0, C0))
