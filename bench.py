@@ -38,6 +38,10 @@ def parse():
     ap.add_argument("--no-ladder", action="store_true", help="skip ladder stages 1-8, 10")
     ap.add_argument("--only", choices=["sgemm", "flash"], default=None,
                     help="run one workload only (for profiling)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="first run a plain 256 MiB device-to-device copy 3 times, the "
+                         "known-size reference dispatch for rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE calibration")
     return ap.parse_args()
 
 
@@ -131,6 +135,14 @@ def main():
     assert torch.cuda.current_stream().cuda_stream == 0, "events must be on the null stream"
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # input generators only, outside the timed region
+
+    if args.copy_calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     result = {}
     N = N_SGEMM

@@ -13,6 +13,16 @@ CANARY = 0x7FA5A5A5   # a quiet-NaN bit pattern no kernel produces
 POISON = 0x7F7F7F7F   # 3.39e38: what the reference test poisons outputs with
 
 
+def fp32_order_bound(K):
+    """Normwise bound for an fp32 result whose products are exact and whose
+    only difference from the exact sum is fp32 summation order: a random-walk
+    rounding model, 4 * sqrt(K) * 2^-24, plus a few ulp for the alpha/beta
+    epilogue. Reduced-precision products (TF32: 2^-11, bf16: 2^-8 relative
+    per product) exceed it by orders of magnitude."""
+    u = 2.0 ** -24
+    return 4.0 * np.sqrt(max(K, 1)) * u + 4.0 * u
+
+
 def dev(a):
     """Host numpy array -> device float32 tensor (contiguous copy)."""
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda")

@@ -51,10 +51,23 @@ def _run_bwd(d_qkv, out, lse, dout, B, T, C, NH, cfg=None):
 
 
 def _check_grads(got, want, C):
+    """Normwise error of dq, dk, dv separately (test_flash.cu:292-314).
+
+    The denominator of each slice is floored at 1e-2 of the largest |ref|
+    over all three: where a slice is exactly zero in exact arithmetic
+    (T = 1: a one-key softmax has zero gradient, so dq = dk = 0 and only dv
+    is non-zero) its fp32 rounding noise is measured against the scale of
+    the gradient as a whole instead of against zero."""
+    floor = 1e-2 * float(np.abs(want).max())
     errs = []
     for s, name in enumerate("qkv"):
-        e, bad = O.normwise(got[:, :, s * C:(s + 1) * C], want[:, :, s * C:(s + 1) * C])
+        g = got[:, :, s * C:(s + 1) * C]
+        w = want[:, :, s * C:(s + 1) * C]
+        e, bad = O.normwise(g, w)
         assert bad == 0, "non-finite d%s" % name
+        wmax = float(np.abs(w).max()) if w.size else 0.0
+        if wmax < floor:
+            e = float(np.abs(g.astype(np.float64) - w).max()) / floor
         errs.append(e)
     return errs
 
