@@ -1,45 +1,50 @@
 // Fused causal attention, forward and backward, for gfx950 -- the
 // counterpart of bare-metal-bard's src/flash.cu (API: src/flash.h).
 //
-// Design: one wave64 owns a 32-row tile and keeps everything in registers.
-//
 // Every contraction is a chain of v_mfma_f32_32x32x2_f32 (fp32 in, exact fp32
 // products, fp32 accumulate). In that instruction lane l supplies
-// A[m = l%32][kk = l/32] and B[kk = l/32][n = l%32], and the 32x32 result
-// leaves lane l holding column n = l%32, register r holding row
-// 8*(r/4) + 4*(l/32) + r%4. Two consequences drive the whole layout:
+// A[m = l%32][kk = l/32] and B[kk = l/32][n = l%32]; the 32x32 result leaves
+// lane l holding column n = l%32, register r holding row
+// res_row(r, l/32) = 8*(r/4) + 4*(l/32) + r%4. A 32-wide contraction over
+// head dims uses dd = (l/32)*hs/2 + st for step st, so each lane's operand is
+// hs/2 contiguous floats of one row: 128-bit LDS or register reads.
 //
-//  * If the score tile is computed TRANSPOSED, S^T = K Q^T (keys x queries),
-//    each lane holds one query's scores for 16 of the 32 keys and its partner
-//    lane (l ^ 32) the other 16. Row max / row sum are then an in-register
-//    reduction plus one cross-half exchange, the online-softmax rescale
-//    touches only the lane's own O^T registers, and the probabilities are
-//    ALREADY in the B-operand layout of O^T += V^T P^T: MFMA step s takes
-//    register s, i.e. key 8*(s/4) + 4*(l/32) + s%4. No LDS round trip, no
-//    barrier. (The reference stages P through shared memory, flash.cu:262-276.)
-//  * The contraction over head dims uses dd = (l/32) * hs/2 + s for step s, so
-//    each lane's q/k/v/dO fragment is hs/2 contiguous floats: 128-bit loads.
+// Work split. A workgroup of WPB waves owns WPB consecutive 32-row tiles of
+// one (batch, head): 32 queries per wave in the forward and the dQ pass,
+// 32 keys per wave in the dK/dV pass. The tiles it streams (keys for the
+// forward and dQ, queries for dK/dV) are staged through LDS once per
+// workgroup, double-buffered with one barrier per tile, and read by every
+// wave of the workgroup with 128-bit, bank-conflict-free LDS reads (rows
+// padded by 4 floats). Causality is a loop bound; only the diagonal and a
+// ragged last tile are masked.
 //
-// Scores are kept in log2 units: q is pre-multiplied by scale*log2(e), so
-// p = exp2(s - m) uses the hardware v_exp_f32. lse is stored in natural-log
-// units (lse = m*ln2 + ln l), exactly the quantity src/flash.cu:309 stores,
-// so forward and backward stay interchangeable with the reference's.
+// Forward (src/flash.cu:115-311 for the maths). The score tile is computed
+// transposed, S^T = K Q^T (keys x queries), so each lane holds one query's
+// scores for 16 keys and lane l^32 the other 16: the row max is an
+// in-register reduction plus one v_permlane32_swap, the online-softmax
+// rescale touches only the lane's own O^T registers, and the probabilities
+// are already in the B-operand layout of O^T += V^T P^T. V is stored
+// transposed in LDS so that the A operand of that product is 128-bit reads.
+// Scores are in log2 units (q pre-multiplied by scale*log2 e), p = exp2(s-m)
+// on v_exp_f32; lse is stored in natural-log units (lse = m ln2 + ln l), the
+// quantity src/flash.cu:309 stores.
 //
-// Causality is a loop bound (a query tile visits key tiles up to its
-// diagonal; a key tile visits query tiles from its diagonal on); only the
-// diagonal tile and a ragged last tile are masked. Tiles are handed out
-// longest-first so the causal triangle does not leave a long tail.
+// Backward (src/flash.cu:434-466). dsum D = rowsum(dO * O), then dK/dV
+// workgroups (S = Q K^T so that P^T and dS^T are in A-operand layout for
+// dV += P^T dO, dK += dS^T Q) and dQ workgroups (S^T layout as in the
+// forward; dQ^T += K^T dS^T). dQ and dK/dV are disjoint slices of dqkv: no
+// atomics, and the result is deterministic.
 //
-// Backward (src/flash.cu:434-466 for the maths): a dsum kernel
-// D = rowsum(dO * O), then ONE launch in which half of the waves compute dK/dV
-// for a 32-key tile (S = Q K^T so that P^T and dS^T are in A-operand layout
-// for dV += P^T dO and dK += dS^T Q) and the other half compute dQ for a
-// 32-query tile (S^T layout as in the forward, dQ^T += K^T dS^T). dQ and dK/dV
-// are disjoint slices of dqkv, so no atomics are needed and both halves share
-// the machine: the long dK/dV tiles are interleaved with the long dQ tiles.
+// Workgroup order. Work items are handed out longest first (the causal
+// triangle would otherwise leave a long tail) and, when B*NH is a multiple of
+// 8, every XCD gets a fixed set of heads: the hardware sends workgroup ids
+// x, x+8, x+16, ... to one XCD, so a head's K/V (or Q/dO) is fetched from
+// HBM into one L2 only.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+
+#include <mutex>
 
 #include "common.hpp"
 #include "../../include/flash.h"
@@ -51,6 +56,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
+constexpr int NXCD = 8;
 
 __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -68,122 +74,220 @@ __device__ __forceinline__ int res_row(int r, int hf) {
     return 8 * (r >> 2) + 4 * hf + (r & 3);
 }
 
-__device__ __forceinline__ float xhalf(float v) {  // value of lane l ^ 32
-    return __shfl_xor(v, 32);
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second; with both operands = v, the two results hold
+// v[l] and v[l^32] (in some order) in every lane l. Max and sum of the pair
+// are therefore symmetric and identical in both lanes.
+__device__ __forceinline__ float pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ float fast_exp2(float x) {
-    return __builtin_amdgcn_exp2f(x);
-}
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Loads N contiguous floats (N % 4 == 0, 16-byte aligned) times `mul`, or
-// zeros when !valid.
-template <int N>
-__device__ __forceinline__ void load_frag(float (&f)[N], const float *p,
-                                          bool valid, float mul) {
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// One 32-row x HS-column fp32 tile in flight from global memory to LDS.
+// Row r of the tile is at src + r*rs; rows >= nrows are zero. Chunk e of the
+// tile (a float4) is row e / (HS/4), columns 4*(e % (HS/4)) + 0..3, so the
+// lanes of a wave read whole rows: coalesced 128-bit loads.
+template <int HS, int NT>
+struct Tile32 {
+    static constexpr int CPR = HS / 4;  // float4 chunks per row
+    static constexpr int PER_T = 32 * CPR / NT;
+    static_assert(PER_T >= 1 && (32 * CPR) % NT == 0, "tile splits evenly over the threads");
+    float4 v[PER_T];
+
+    __device__ __forceinline__ void load(const float *src, size_t rs, int nrows, int tid) {
 #pragma unroll
-    for (int i = 0; i < N; i += 4) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (valid) v = bmb::ld4(p + i);
-        f[i + 0] = v.x * mul; f[i + 1] = v.y * mul;
-        f[i + 2] = v.z * mul; f[i + 3] = v.w * mul;
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
+            v[i] = r < nrows ? bmb::ld4(src + (size_t)r * rs + c) : zero4();
+        }
     }
+    // Row-major copy, LDS row stride ld floats.
+    __device__ __forceinline__ void store_rows(float *lds, int ld, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
+            bmb::st4(lds + r * ld + c, v[i]);
+        }
+    }
+    // Transposed copy: element (r, c) goes to lds[c*ld + r].
+    __device__ __forceinline__ void store_cols(float *lds, int ld, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
+            lds[(c + 0) * ld + r] = v[i].x;
+            lds[(c + 1) * ld + r] = v[i].y;
+            lds[(c + 2) * ld + r] = v[i].z;
+            lds[(c + 3) * ld + r] = v[i].w;
+        }
+    }
+};
+
+// Work item of workgroup `bid` among nblk tiles x BH heads.
+// longest_hi: tile nblk-1 is the longest (forward, dQ); otherwise tile 0 is
+// (dK/dV). Items are handed out longest first. With SNAKE, the k-th round of
+// `cus` workgroups on one XCD walks the longest-first list in alternating
+// direction, so that when a whole grid is resident at once every CU of the XCD
+// receives a near-equal sum of work instead of the longest items together.
+template <bool SNAKE>
+__device__ __forceinline__ void work_item(int bid, int BH, int nblk, bool longest_hi, int cus,
+                                          int &blk, int &bh) {
+    int rank;
+    if (BH % NXCD == 0) {
+        const int xcd = bid % NXCD, hpx = BH / NXCD;
+        int w = bid / NXCD;
+        if (SNAKE) {
+            const int per_xcd = hpx * nblk, round = w / cus, pos = w % cus;
+            const int n = min(cus, per_xcd - round * cus);
+            w = round * cus + ((round & 1) ? n - 1 - pos : pos);
+        }
+        rank = w / hpx;
+        bh = (w % hpx) * NXCD + xcd;
+    } else {
+        rank = bid / BH;
+        bh = bid % BH;
+    }
+    blk = longest_hi ? nblk - 1 - rank : rank;
 }
 
 // ------------------------------------------------------------------ forward
-//
-// Wave g of the launch owns query tile qt of head bh. qkv row t of (b, h):
-// q at +0, k at +C, v at +2C, each hs floats (src/flash.cu:151-152).
-template <int HS, int WPB>
-__global__ __launch_bounds__(WPB * 64) void flash_fwd_k(
-    float *__restrict__ out, float *__restrict__ lse,
-    const float *__restrict__ qkv, int T, int NH, int BH, float qscale) {
-    constexpr int HH = HS / 2, DT = HS / 32;
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
-    const int nqt = (T + 31) / 32;
-    const int g = blockIdx.x * WPB + (threadIdx.x >> 6);
-    if (g >= BH * nqt) return;
-    const int qt = nqt - 1 - g / BH;  // longest (most keys) first
-    const int bh = g % BH, b = bh / NH, h = bh % NH;
-    const int C = NH * HS;
+
+template <int HS>
+struct FwdSmem {
+    static constexpr int LDK = HS + 4;   // K rows (keys), 128-bit reads
+    static constexpr int LDV = 32 + 4;   // V^T rows (head dims), 128-bit reads
+    static constexpr int BUF = 32 * LDK + HS * LDV;
+    static constexpr size_t BYTES = 2 * (size_t)BUF * sizeof(float);
+};
+
+template <int HS, int WPB, bool SNAKE, int MINW>
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
+flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__restrict__ qkv,
+            int T, int NH, int BH, float qscale, int cus) {
+    constexpr int NT = WPB * 64, QB = 32 * WPB, HH = HS / 2, DT = HS / 32;
+    using S = FwdSmem<HS>;
+    extern __shared__ float smem[];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int nqb = (T + QB - 1) / QB;
+    int qb, bh;
+    work_item<SNAKE>(blockIdx.x, BH, nqb, true, cus, qb, bh);
+    const int b = bh / NH, h = bh % NH, C = NH * HS;
     const size_t rs = 3 * (size_t)C;
     const float *base = qkv + (size_t)b * T * rs + h * HS;
 
-    const int q0 = qt * 32, qi = q0 + l32;
+    const int q0w = qb * QB + wave * 32;  // this wave's first query
+    const int qi = q0w + l32;
+    const bool active = q0w < T;
+
+    // B operand of S^T = K Q^T: lane holds q[qi][hf*HH + st] * qscale.
     float qf[HH];
-    load_frag<HH>(qf, base + (size_t)qi * rs + hf * HH, qi < T, qscale);
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        const float4 v = qi < T ? bmb::ld4(base + (size_t)qi * rs + hf * HH + j) : zero4();
+        qf[j + 0] = v.x * qscale; qf[j + 1] = v.y * qscale;
+        qf[j + 2] = v.z * qscale; qf[j + 3] = v.w * qscale;
+    }
 
     f32x16 o[DT];
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[d] = zero16();
     float m = -INFINITY, l = 0.0f;
 
-    const int kend = min(T, q0 + 32);
-    float kf[HH];
-    load_frag<HH>(kf, base + (size_t)l32 * rs + C + hf * HH, l32 < T, 1.0f);
+    const int kend = min(T, qb * QB + QB);
+    const int nkt = (kend + 31) / 32;
+    const int my_nkt = active ? (min(T, q0w + 32) + 31) / 32 : 0;
 
-    for (int kb = 0; kb < kend; kb += 32) {
-        // V^T operand for this tile: step s uses key kb + res_row(s, hf).
-        float vf[16][DT];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int key = kb + res_row(s, hf);
-#pragma unroll
-            for (int d = 0; d < DT; ++d)
-                vf[s][d] = key < T ? base[(size_t)key * rs + 2 * C + d * 32 + l32] : 0.0f;
+    Tile32<HS, NT> kt, vt;
+    kt.load(base + C, rs, min(32, T), tid);
+    vt.load(base + 2 * C, rs, min(32, T), tid);
+    kt.store_rows(smem, S::LDK, tid);
+    vt.store_cols(smem + 32 * S::LDK, S::LDV, tid);
+    __syncthreads();
+
+    for (int t = 0; t < nkt; ++t) {
+        const int kb = t * 32;
+        const bool more = t + 1 < nkt;
+        if (more) {
+            const int nr = min(32, T - kb - 32);
+            kt.load(base + (size_t)(kb + 32) * rs + C, rs, nr, tid);
+            vt.load(base + (size_t)(kb + 32) * rs + 2 * C, rs, nr, tid);
         }
+        if (t < my_nkt) {
+            const float *ks = smem + (t & 1) * S::BUF;
+            const float *vs = ks + 32 * S::LDK;
 
-        // S^T = K Q^T, 32 keys x 32 queries, log2 units.
-        f32x16 s = zero16();
+            // S^T = K Q^T, 32 keys x 32 queries, log2 units.
+            f32x16 s = zero16();
+            const float *krow = ks + l32 * S::LDK + hf * HH;
 #pragma unroll
-        for (int st = 0; st < HH; ++st) s = mfma(kf[st], qf[st], s);
-
-        // Next tile's K while this one's softmax and PV run.
-        if (kb + 32 < kend) {
-            const int nk = kb + 32 + l32;
-            load_frag<HH>(kf, base + (size_t)nk * rs + C + hf * HH, nk < T, 1.0f);
-        }
-
-        if (kb + 32 > q0 || kb + 32 > T) {  // diagonal or ragged tile
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kb + res_row(r, hf);
-                if (key > qi || key >= T) s[r] = -INFINITY;
+            for (int j = 0; j < HH; j += 4) {
+                const float4 kv = bmb::ld4(krow + j);
+                s = mfma(kv.x, qf[j + 0], s);
+                s = mfma(kv.y, qf[j + 1], s);
+                s = mfma(kv.z, qf[j + 2], s);
+                s = mfma(kv.w, qf[j + 3], s);
             }
-        }
-        float mb = s[0];
+            if (kb + 32 > q0w || kb + 32 > T) {  // diagonal or ragged tile
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
-        mb = fmaxf(mb, xhalf(mb));
-        const float mn = fmaxf(m, mb);
-        float p[16], ls = 0.0f, alpha = 1.0f;
-        if (mn == -INFINITY) {
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + res_row(r, hf);
+                    if (key > qi || key >= T) s[r] = -INFINITY;
+                }
+            }
+            float mb = s[0];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = 0.0f;
-        } else {
-            alpha = fast_exp2(m - mn);  // 0 when m was -inf
+            for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+            const float mn = fmaxf(m, pair_max(mb));  // finite: key kb is live in tile 0
+            const float alpha = exp2_hw(m - mn);      // 0 on the first tile
+            float p[16], ls = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                p[r] = fast_exp2(s[r] - mn);
+                p[r] = exp2_hw(s[r] - mn);
                 ls += p[r];
             }
-        }
-        ls += xhalf(ls);
-        l = l * alpha + ls;
-        m = mn;
+            l = l * alpha + ls;  // this half's keys; halves are combined at the end
+            m = mn;
 #pragma unroll
-        for (int d = 0; d < DT; ++d)
+            for (int d = 0; d < DT; ++d)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+                for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
 
-        // O^T += V^T P^T
+            // O^T += V^T P^T. Step st pairs key res_row(st, hf) of this half;
+            // keys 8j + 4hf + 0..3 are 4 consecutive floats of a V^T row.
 #pragma unroll
-        for (int st = 0; st < 16; ++st)
+            for (int d = 0; d < DT; ++d) {
+                const float *vrow = vs + (d * 32 + l32) * S::LDV + 4 * hf;
 #pragma unroll
-            for (int d = 0; d < DT; ++d) o[d] = mfma(vf[st][d], p[st], o[d]);
+                for (int j = 0; j < 4; ++j) {
+                    const float4 vv = bmb::ld4(vrow + 8 * j);
+                    o[d] = mfma(vv.x, p[4 * j + 0], o[d]);
+                    o[d] = mfma(vv.y, p[4 * j + 1], o[d]);
+                    o[d] = mfma(vv.z, p[4 * j + 2], o[d]);
+                    o[d] = mfma(vv.w, p[4 * j + 3], o[d]);
+                }
+            }
+        }
+        if (more) {
+            float *nb = smem + ((t + 1) & 1) * S::BUF;
+            kt.store_rows(nb, S::LDK, tid);
+            vt.store_cols(nb + 32 * S::LDK, S::LDV, tid);
+        }
+        __syncthreads();
     }
 
-    if (qi < T) {
+    l = pair_sum(l);
+    if (active && qi < T) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         float *dst = out + ((size_t)b * T + qi) * C + h * HS;
 #pragma unroll
@@ -201,6 +305,7 @@ __global__ __launch_bounds__(WPB * 64) void flash_fwd_k(
 
 // D[b,h,t] = sum_i dO[b,t,h*hs+i] * O[b,t,h*hs+i] (src/flash.cu:471-487).
 // HS/4 lanes per row, one float4 each, reduced with cross-lane xor shuffles.
+// Rows are walked in (b, h, t) order so that the D writes are contiguous.
 template <int HS>
 __global__ __launch_bounds__(256) void flash_dsum_k(float *__restrict__ dsum,
                                                     const float *__restrict__ dout,
@@ -208,36 +313,46 @@ __global__ __launch_bounds__(256) void flash_dsum_k(float *__restrict__ dsum,
                                                     int T, int NH, long long rows) {
     constexpr int LPR = HS / 4;  // lanes per row
     const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long row = gid / LPR;  // row = (b*T + t)*NH + h: memory order
+    const long long row = gid / LPR;  // row = (b*NH + h)*T + t
     const int sub = (int)(gid % LPR);
     float s = 0.0f;
     if (row < rows) {
-        const size_t off = (size_t)row * HS + sub * 4;
+        const int t = (int)(row % T);
+        const long long bh = row / T;
+        const int h = (int)(bh % NH);
+        const long long b = bh / NH;
+        const size_t off = ((size_t)b * T + t) * NH * HS + (size_t)h * HS + sub * 4;
         const float4 a = bmb::ld4(dout + off), c = bmb::ld4(out + off);
         s = a.x * c.x + a.y * c.y + a.z * c.z + a.w * c.w;
     }
 #pragma unroll
     for (int w = 1; w < LPR; w <<= 1) s += __shfl_xor(s, w);
-    if (row < rows && sub == 0) {
-        const int h = (int)(row % NH);
-        const long long bt = row / NH;
-        const int t = (int)(bt % T);
-        const long long b = bt / T;
-        dsum[((size_t)b * NH + h) * T + t] = s;
-    }
+    if (row < rows && sub == 0) dsum[row] = s;
 }
 
-// dK, dV for key tile kt of head bh.
 template <int HS>
-__device__ __forceinline__ void bwd_kv_tile(float *__restrict__ dqkv,
-                                            const float *__restrict__ qkv,
-                                            const float *__restrict__ dout,
-                                            const float *__restrict__ lse,
-                                            const float *__restrict__ dsum,
-                                            int T, int NH, int kt, int bh,
-                                            float scale, float qscale) {
-    constexpr int HH = HS / 2, DT = HS / 32;
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
+struct BwdSmem {
+    static constexpr int LD = HS + 4;
+    // dK/dV pass: Q rows, dO rows, lse (log2 units), D.
+    static constexpr int KV_BUF = 2 * 32 * LD + 64;
+    // dQ pass: K rows, V rows.
+    static constexpr int Q_BUF = 2 * 32 * LD;
+    static constexpr int BUF = KV_BUF > Q_BUF ? KV_BUF : Q_BUF;
+    static constexpr size_t BYTES = 2 * (size_t)BUF * sizeof(float);
+};
+
+// dK, dV for the WPB*32 keys of key block kblk of head bh.
+template <int HS, int WPB>
+__device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dqkv,
+                                             const float *__restrict__ qkv,
+                                             const float *__restrict__ dout,
+                                             const float *__restrict__ lse,
+                                             const float *__restrict__ dsum, int T, int NH,
+                                             int kblk, int bh, float scale, float qscale) {
+    constexpr int NT = WPB * 64, KB = 32 * WPB, HH = HS / 2, DT = HS / 32;
+    using S = BwdSmem<HS>;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
     const int b = bh / NH, h = bh % NH, C = NH * HS;
     const size_t rs = 3 * (size_t)C;
     const float *base = qkv + (size_t)b * T * rs + h * HS;
@@ -245,72 +360,115 @@ __device__ __forceinline__ void bwd_kv_tile(float *__restrict__ dqkv,
     const float *lrow = lse + (size_t)bh * T;
     const float *drow = dsum + (size_t)bh * T;
 
-    const int k0 = kt * 32, key = k0 + l32;
-    // B operands of S = Q K^T and dP = dO V^T: K (log2-scaled) and V.
+    const int k0w = kblk * KB + wave * 32, key = k0w + l32;
+    const bool active = k0w < T;
+    // B operands of S = Q K^T and dP = dO V^T: K (log2-scaled) and V rows.
     float kf[HH], vf[HH];
-    load_frag<HH>(kf, base + (size_t)key * rs + C + hf * HH, key < T, qscale);
-    load_frag<HH>(vf, base + (size_t)key * rs + 2 * C + hf * HH, key < T, 1.0f);
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        float4 kv = zero4(), vv = zero4();
+        if (key < T) {
+            kv = bmb::ld4(base + (size_t)key * rs + C + hf * HH + j);
+            vv = bmb::ld4(base + (size_t)key * rs + 2 * C + hf * HH + j);
+        }
+        kf[j + 0] = kv.x * qscale; kf[j + 1] = kv.y * qscale;
+        kf[j + 2] = kv.z * qscale; kf[j + 3] = kv.w * qscale;
+        vf[j + 0] = vv.x; vf[j + 1] = vv.y; vf[j + 2] = vv.z; vf[j + 3] = vv.w;
+    }
 
     f32x16 dv[DT], dk[DT];
 #pragma unroll
     for (int d = 0; d < DT; ++d) { dv[d] = zero16(); dk[d] = zero16(); }
 
-    for (int qb = k0; qb < T; qb += 32) {
-        const int qa_row = qb + l32;
-        float qa[HH], da[HH];
-        load_frag<HH>(qa, base + (size_t)qa_row * rs + hf * HH, qa_row < T, 1.0f);
-        load_frag<HH>(da, dob + (size_t)qa_row * C + hf * HH, qa_row < T, 1.0f);
-        // lse (as log2) and D of the 16 query rows this lane's results hold.
-        float L2[16], Dv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int q = qb + res_row(r, hf);
-            L2[r] = q < T ? lrow[q] * LOG2E : 0.0f;
-            Dv[r] = q < T ? drow[q] : 0.0f;
+    // Query tiles from the workgroup's first key on; wave w starts at tile w.
+    const int q_start = kblk * KB;
+    const int nqt = (T - q_start + 31) / 32;
+    Tile32<HS, NT> qt, ot;
+    float lv = 0.0f;  // staging of lse*log2e (tid < 32) and D (32 <= tid < 64)
+    auto load_tile = [&](int qb) {
+        const int nr = min(32, T - qb);
+        qt.load(base + (size_t)qb * rs, rs, nr, tid);
+        ot.load(dob + (size_t)qb * C, C, nr, tid);
+        if (tid < 64) {
+            const int q = qb + (tid & 31);
+            lv = q < T ? (tid < 32 ? lrow[q] * LOG2E : drow[q]) : 0.0f;
         }
+    };
+    auto store_tile = [&](float *buf) {
+        qt.store_rows(buf, S::LD, tid);
+        ot.store_rows(buf + 32 * S::LD, S::LD, tid);
+        if (tid < 64) buf[2 * 32 * S::LD + tid] = lv;
+    };
+    load_tile(q_start);
+    store_tile(smem);
+    __syncthreads();
 
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int st = 0; st < HH; ++st) {
-            s = mfma(qa[st], kf[st], s);
-            dp = mfma(da[st], vf[st], dp);
-        }
+    for (int t = 0; t < nqt; ++t) {
+        const int qb = q_start + 32 * t;
+        const bool more = t + 1 < nqt;
+        if (more) load_tile(qb + 32);
+        if (active && t >= wave) {
+            const float *qs = smem + (t & 1) * S::BUF;
+            const float *os = qs + 32 * S::LD;
+            const float *ls = qs + 2 * 32 * S::LD;
 
-        // B operands of dV += P^T dO and dK += dS^T Q: rows q(st) of dO, Q.
-        float dob_f[16][DT], qb_f[16][DT];
+            // S = Q K^T and dP = dO V^T: 32 queries x 32 keys; lane holds key
+            // l32, register r holds query qb + res_row(r, hf).
+            f32x16 s = zero16(), dp = zero16();
+            const float *qrow = qs + l32 * S::LD + hf * HH;
+            const float *orow = os + l32 * S::LD + hf * HH;
 #pragma unroll
-        for (int st = 0; st < 16; ++st) {
-            const int q = qb + res_row(st, hf);
+            for (int j = 0; j < HH; j += 4) {
+                const float4 qa = bmb::ld4(qrow + j), da = bmb::ld4(orow + j);
+                s = mfma(qa.x, kf[j + 0], s);
+                dp = mfma(da.x, vf[j + 0], dp);
+                s = mfma(qa.y, kf[j + 1], s);
+                dp = mfma(da.y, vf[j + 1], dp);
+                s = mfma(qa.z, kf[j + 2], s);
+                dp = mfma(da.z, vf[j + 2], dp);
+                s = mfma(qa.w, kf[j + 3], s);
+                dp = mfma(da.w, vf[j + 3], dp);
+            }
+
+            const bool edge = qb == k0w || qb + 32 > T || k0w + 32 > T;
+            float p[16], ds[16];
 #pragma unroll
-            for (int d = 0; d < DT; ++d) {
-                dob_f[st][d] = q < T ? dob[(size_t)q * C + d * 32 + l32] : 0.0f;
-                qb_f[st][d] = q < T ? base[(size_t)q * rs + d * 32 + l32] : 0.0f;
+            for (int j = 0; j < 4; ++j) {
+                const float4 L4 = bmb::ld4(ls + 8 * j + 4 * hf);
+                const float4 D4 = bmb::ld4(ls + 32 + 8 * j + 4 * hf);
+                const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
+                const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * j + i;
+                    const int q = qb + res_row(r, hf);
+                    const bool live = !edge || (q < T && key < T && key <= q);
+                    p[r] = live ? exp2_hw(s[r] - Lr[i]) : 0.0f;
+                    ds[r] = p[r] * (dp[r] - Dr[i]);
+                }
+            }
+
+            // dV += P^T dO, dK += dS^T Q: step st contracts over query
+            // res_row(st, hf); B operands are those rows of dO and Q.
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {
+                const int qr = res_row(st, hf);
+#pragma unroll
+                for (int d = 0; d < DT; ++d) {
+                    dv[d] = mfma(p[st], os[qr * S::LD + d * 32 + l32], dv[d]);
+                    dk[d] = mfma(ds[st], qs[qr * S::LD + d * 32 + l32], dk[d]);
+                }
             }
         }
-
-        const bool edge = (qb < k0 + 32) || (qb + 32 > T);
-        float p[16], ds[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int q = qb + res_row(r, hf);
-            const bool live = !edge || (q < T && key < T && key <= q);
-            p[r] = live ? fast_exp2(s[r] - L2[r]) : 0.0f;
-            ds[r] = p[r] * (dp[r] - Dv[r]);
-        }
-
-#pragma unroll
-        for (int st = 0; st < 16; ++st)
-#pragma unroll
-            for (int d = 0; d < DT; ++d) {
-                dv[d] = mfma(p[st], dob_f[st][d], dv[d]);
-                dk[d] = mfma(ds[st], qb_f[st][d], dk[d]);
-            }
+        if (more) store_tile(smem + ((t + 1) & 1) * S::BUF);
+        __syncthreads();
     }
 
-    // Lane holds column d*32 + l32 of rows key k0 + res_row(r, hf).
+    if (!active) return;
+    // Lane holds column d*32 + l32 of key rows k0w + res_row(r, hf).
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const int kr = k0 + res_row(r, hf);
+        const int kr = k0w + res_row(r, hf);
         if (kr >= T) continue;
         float *dkp = dqkv + ((size_t)b * T + kr) * rs + C + h * HS;
 #pragma unroll
@@ -321,27 +479,38 @@ __device__ __forceinline__ void bwd_kv_tile(float *__restrict__ dqkv,
     }
 }
 
-// dQ for query tile qt of head bh.
-template <int HS>
-__device__ __forceinline__ void bwd_q_tile(float *__restrict__ dqkv,
-                                           const float *__restrict__ qkv,
-                                           const float *__restrict__ dout,
-                                           const float *__restrict__ lse,
-                                           const float *__restrict__ dsum,
-                                           int T, int NH, int qt, int bh,
-                                           float scale, float qscale) {
-    constexpr int HH = HS / 2, DT = HS / 32;
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
+// dQ for the WPB*32 queries of query block qblk of head bh.
+template <int HS, int WPB>
+__device__ __forceinline__ void bwd_q_block(float *smem, float *__restrict__ dqkv,
+                                            const float *__restrict__ qkv,
+                                            const float *__restrict__ dout,
+                                            const float *__restrict__ lse,
+                                            const float *__restrict__ dsum, int T, int NH,
+                                            int qblk, int bh, float scale, float qscale) {
+    constexpr int NT = WPB * 64, QB = 32 * WPB, HH = HS / 2, DT = HS / 32;
+    using S = BwdSmem<HS>;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
     const int b = bh / NH, h = bh % NH, C = NH * HS;
     const size_t rs = 3 * (size_t)C;
     const float *base = qkv + (size_t)b * T * rs + h * HS;
     const float *dob = dout + (size_t)b * T * C + h * HS;
 
-    const int q0 = qt * 32, qi = q0 + l32;
-    const bool qv = qi < T;
+    const int q0w = qblk * QB + wave * 32, qi = q0w + l32;
+    const bool active = q0w < T, qv = qi < T;
+    // B operands of S^T = K Q^T and dP^T = V dO^T: this lane's query row.
     float qf[HH], df[HH];
-    load_frag<HH>(qf, base + (size_t)qi * rs + hf * HH, qv, qscale);
-    load_frag<HH>(df, dob + (size_t)qi * C + hf * HH, qv, 1.0f);
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        float4 qa = zero4(), da = zero4();
+        if (qv) {
+            qa = bmb::ld4(base + (size_t)qi * rs + hf * HH + j);
+            da = bmb::ld4(dob + (size_t)qi * C + hf * HH + j);
+        }
+        qf[j + 0] = qa.x * qscale; qf[j + 1] = qa.y * qscale;
+        qf[j + 2] = qa.z * qscale; qf[j + 3] = qa.w * qscale;
+        df[j + 0] = da.x; df[j + 1] = da.y; df[j + 2] = da.z; df[j + 3] = da.w;
+    }
     const float L2 = qv ? lse[(size_t)bh * T + qi] * LOG2E : 0.0f;
     const float Dq = qv ? dsum[(size_t)bh * T + qi] : 0.0f;
 
@@ -349,47 +518,71 @@ __device__ __forceinline__ void bwd_q_tile(float *__restrict__ dqkv,
 #pragma unroll
     for (int d = 0; d < DT; ++d) dq[d] = zero16();
 
-    const int kend = min(T, q0 + 32);
-    for (int kb = 0; kb < kend; kb += 32) {
-        const int ka_row = kb + l32;
-        float ka[HH], va[HH];
-        load_frag<HH>(ka, base + (size_t)ka_row * rs + C + hf * HH, ka_row < T, 1.0f);
-        load_frag<HH>(va, base + (size_t)ka_row * rs + 2 * C + hf * HH, ka_row < T, 1.0f);
+    const int kend = min(T, qblk * QB + QB);
+    const int nkt = (kend + 31) / 32;
+    const int my_nkt = active ? (min(T, q0w + 32) + 31) / 32 : 0;
+    Tile32<HS, NT> kt, vt;
+    kt.load(base + C, rs, min(32, T), tid);
+    vt.load(base + 2 * C, rs, min(32, T), tid);
+    kt.store_rows(smem, S::LD, tid);
+    vt.store_rows(smem + 32 * S::LD, S::LD, tid);
+    __syncthreads();
 
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int st = 0; st < HH; ++st) {
-            s = mfma(ka[st], qf[st], s);
-            dp = mfma(va[st], df[st], dp);
+    for (int t = 0; t < nkt; ++t) {
+        const int kb = 32 * t;
+        const bool more = t + 1 < nkt;
+        if (more) {
+            const int nr = min(32, T - kb - 32);
+            kt.load(base + (size_t)(kb + 32) * rs + C, rs, nr, tid);
+            vt.load(base + (size_t)(kb + 32) * rs + 2 * C, rs, nr, tid);
         }
-
-        // A operand of dQ^T += K^T dS^T: rows key(st) of K.
-        float kb_f[16][DT];
+        if (t < my_nkt) {
+            const float *ks = smem + (t & 1) * S::BUF;
+            const float *vs = ks + 32 * S::LD;
+            // S^T = K Q^T, dP^T = V dO^T: lane holds query l32, register r
+            // holds key kb + res_row(r, hf).
+            f32x16 s = zero16(), dp = zero16();
+            const float *krow = ks + l32 * S::LD + hf * HH;
+            const float *vrow = vs + l32 * S::LD + hf * HH;
 #pragma unroll
-        for (int st = 0; st < 16; ++st) {
-            const int kr = kb + res_row(st, hf);
+            for (int j = 0; j < HH; j += 4) {
+                const float4 ka = bmb::ld4(krow + j), va = bmb::ld4(vrow + j);
+                s = mfma(ka.x, qf[j + 0], s);
+                dp = mfma(va.x, df[j + 0], dp);
+                s = mfma(ka.y, qf[j + 1], s);
+                dp = mfma(va.y, df[j + 1], dp);
+                s = mfma(ka.z, qf[j + 2], s);
+                dp = mfma(va.z, df[j + 2], dp);
+                s = mfma(ka.w, qf[j + 3], s);
+                dp = mfma(va.w, df[j + 3], dp);
+            }
+            const bool edge = kb + 32 > q0w || kb + 32 > T;
+            float ds[16];
 #pragma unroll
-            for (int d = 0; d < DT; ++d)
-                kb_f[st][d] = kr < T ? base[(size_t)kr * rs + C + d * 32 + l32] : 0.0f;
+            for (int r = 0; r < 16; ++r) {
+                const int kr = kb + res_row(r, hf);
+                const bool live = !edge || (qv && kr < T && kr <= qi);
+                const float p = live ? exp2_hw(s[r] - L2) : 0.0f;
+                ds[r] = p * (dp[r] - Dq);
+            }
+            // dQ^T += K^T dS^T: step st contracts over key res_row(st, hf).
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {
+                const int kr = res_row(st, hf);
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+                    dq[d] = mfma(ks[kr * S::LD + d * 32 + l32], ds[st], dq[d]);
+            }
         }
-
-        const bool edge = (kb + 32 > q0) || (kb + 32 > T);
-        float ds[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = kb + res_row(r, hf);
-            const bool live = !edge || (qv && kr < T && kr <= qi);
-            const float p = live ? fast_exp2(s[r] - L2) : 0.0f;
-            ds[r] = p * (dp[r] - Dq);
+        if (more) {
+            float *nb = smem + ((t + 1) & 1) * S::BUF;
+            kt.store_rows(nb, S::LD, tid);
+            vt.store_rows(nb + 32 * S::LD, S::LD, tid);
         }
-
-#pragma unroll
-        for (int st = 0; st < 16; ++st)
-#pragma unroll
-            for (int d = 0; d < DT; ++d) dq[d] = mfma(kb_f[st][d], ds[st], dq[d]);
+        __syncthreads();
     }
 
-    if (qv) {
+    if (active && qv) {
         float *dst = dqkv + ((size_t)b * T + qi) * rs + h * HS;
 #pragma unroll
         for (int d = 0; d < DT; ++d)
@@ -401,43 +594,90 @@ __device__ __forceinline__ void bwd_q_tile(float *__restrict__ dqkv,
     }
 }
 
-// MODE 0: waves alternate dK/dV and dQ work, both longest-first.
+// MODE 0: dK/dV and dQ workgroups interleaved in one launch.
 // MODE 1: dK/dV only.  MODE 2: dQ only.
-template <int HS, int WPB, int MODE>
-__global__ __launch_bounds__(WPB * 64) void flash_bwd_k(
-    float *__restrict__ dqkv, const float *__restrict__ qkv,
-    const float *__restrict__ dout, const float *__restrict__ lse,
-    const float *__restrict__ dsum, int T, int NH, int BH, float scale,
-    float qscale) {
-    const int nt = (T + 31) / 32;
-    const int items = BH * nt;
-    const int g = blockIdx.x * WPB + (threadIdx.x >> 6);
-    int kind, u;
-    if (MODE == 0) { kind = g & 1; u = g >> 1; }
-    else           { kind = MODE - 1; u = g; }
-    if (u >= items) return;
-    const int tile = u / BH, bh = u % BH;
-    if (kind == 0)
-        bwd_kv_tile<HS>(dqkv, qkv, dout, lse, dsum, T, NH, tile, bh, scale, qscale);
-    else
-        bwd_q_tile<HS>(dqkv, qkv, dout, lse, dsum, T, NH, nt - 1 - tile, bh, scale, qscale);
+template <int HS, int WPB, int MODE, int MINW>
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
+flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
+            const float *__restrict__ dout, const float *__restrict__ lse,
+            const float *__restrict__ dsum, int T, int NH, int BH, float scale, float qscale) {
+    extern __shared__ float smem[];
+    constexpr int RB = 32 * WPB;
+    const int nblk = (T + RB - 1) / RB;
+    int role, bid = blockIdx.x;
+    if (MODE == 0) {
+        // Pairs (dK/dV item, dQ item) of equal rank in their longest-first
+        // orders. With B*NH a multiple of 8 the grid is a multiple of 16 and
+        // ids x, x+8, ... (one XCD) keep to one set of heads in both roles.
+        if (BH % NXCD == 0) {
+            const int xcd = bid % NXCD, w = bid / NXCD;
+            role = w & 1;
+            bid = (w >> 1) * NXCD + xcd;
+        } else {
+            role = bid & 1;
+            bid >>= 1;
+        }
+    } else {
+        role = MODE - 1;
+    }
+    int blk, bh;
+    if (role == 0) {
+        work_item<false>(bid, BH, nblk, false, 0, blk, bh);
+        bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
+    } else {
+        work_item<false>(bid, BH, nblk, true, 0, blk, bh);
+        bwd_q_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
+    }
 }
 
 // ------------------------------------------------------------- host side
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Kernels whose LDS exceeds the 64 KiB default get their limit raised once
+// per device.
+template <typename K>
+void allow_smem(K kern, size_t bytes) {
+    if (bytes <= 65536) return;
+    static std::once_flag once[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+    std::call_once(once[dev], [&] {
+        bmb::note_launch_status(hipFuncSetAttribute(
+            reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+            (int)bytes));
+    });
+}
+
+int cus_per_xcd() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess || cus < NXCD)
+            cus = 256;
+        cached[dev] = cus / NXCD;
+    }
+    return cached[dev];
+}
+
+// Forward tile configs. wpb: 32-query waves per workgroup (they share every
+// staged K/V tile); snake: snake work order (see work_item); minw: minimum
+// waves per SIMD the register allocation must allow.
 struct FwdCfg {
     const char *name;
     int wpb;
+    bool snake;
+    int minw;
 };
-// Waves per workgroup only changes how many independent 32-query waves share
-// a workgroup slot; the per-wave work is identical.
 const FwdCfg FWD_CFGS[] = {
-    {"q32/wave mfma32 wg4", 4},
-    {"q32/wave mfma32 wg1", 1},
-    {"q32/wave mfma32 wg2", 2},
-    {"q32/wave mfma32 wg8", 8},
+    {"q128/wg lds-kv mfma32 snake", 4, true, 1},
+    {"q64/wg lds-kv mfma32 snake", 2, true, 1},
+    {"q128/wg lds-kv mfma32", 4, false, 1},
+    {"q128/wg lds-kv mfma32 snake 4w/simd", 4, true, 4},
+    {"q64/wg lds-kv mfma32 snake 4w/simd", 2, true, 4},
 };
 constexpr int N_FWD = sizeof(FWD_CFGS) / sizeof(FWD_CFGS[0]);
 constexpr int FWD_DEFAULT = 0;
@@ -446,60 +686,75 @@ struct BwdCfg {
     const char *name;
     int wpb;
     bool fused;
+    int minw;
 };
 const BwdCfg BWD_CFGS[] = {
-    {"kv32+q32 fused mfma32 wg4", 4, true},
-    {"kv32+q32 fused mfma32 wg2", 2, true},
-    {"kv32 then q32 mfma32 wg4", 4, false},
-    {"kv32+q32 fused mfma32 wg1", 1, true},
+    {"kv128+q128/wg fused lds mfma32 2w/simd", 4, true, 2},
+    {"kv64+q64/wg fused lds mfma32 2w/simd", 2, true, 2},
+    {"kv128/wg then q128/wg lds mfma32 2w/simd", 4, false, 2},
+    {"kv64/wg then q64/wg lds mfma32 2w/simd", 2, false, 2},
+    {"kv128+q128/wg fused lds mfma32", 4, true, 1},
 };
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
 constexpr int BWD_DEFAULT = 0;
 
-template <int HS, int WPB>
+int grid_blocks(int BH, int T, int rows_per_block) {
+    return BH * ((T + rows_per_block - 1) / rows_per_block);
+}
+
+template <int HS, int WPB, bool SNAKE, int MINW>
 void run_fwd(float *out, float *lse, const float *qkv, int B, int T, int NH) {
-    const int BH = B * NH, nqt = (T + 31) / 32;
-    const long long waves = (long long)BH * nqt;
+    const int BH = B * NH;
     const float qscale = (1.0f / sqrtf((float)HS)) * LOG2E;
-    bmb::launch(flash_fwd_k<HS, WPB>, dim3((unsigned)((waves + WPB - 1) / WPB)),
-                dim3(WPB * 64), 0, nullptr, out, lse, qkv, T, NH, BH, qscale);
+    const size_t smem = FwdSmem<HS>::BYTES;
+    auto kern = flash_fwd_k<HS, WPB, SNAKE, MINW>;
+    allow_smem(kern, smem);
+    bmb::launch(kern, dim3(grid_blocks(BH, T, 32 * WPB)), dim3(WPB * 64), smem, nullptr, out,
+                lse, qkv, T, NH, BH, qscale, cus_per_xcd());
 }
 
 template <int HS>
 bool fwd_hs(int cfg, float *out, float *lse, const float *qkv, int B, int T, int NH) {
-    switch (FWD_CFGS[cfg].wpb) {
-    case 1: run_fwd<HS, 1>(out, lse, qkv, B, T, NH); return true;
-    case 2: run_fwd<HS, 2>(out, lse, qkv, B, T, NH); return true;
-    case 4: run_fwd<HS, 4>(out, lse, qkv, B, T, NH); return true;
-    case 8: run_fwd<HS, 8>(out, lse, qkv, B, T, NH); return true;
-    default: return false;
+    const FwdCfg &c = FWD_CFGS[cfg];
+#define BMB_FWD(W, S, M)                                                       \
+    if (c.wpb == W && c.snake == S && c.minw == M) {                           \
+        run_fwd<HS, W, S, M>(out, lse, qkv, B, T, NH);                         \
+        return true;                                                           \
     }
+    BMB_FWD(4, true, 1)
+    BMB_FWD(2, true, 1)
+    BMB_FWD(4, false, 1)
+    BMB_FWD(4, true, 4)
+    BMB_FWD(2, true, 4)
+#undef BMB_FWD
+    return false;
 }
 
-template <int HS, int WPB, int MODE>
-void run_bwd_mode(float *dqkv, const float *dout, const float *qkv,
-                  const float *lse, const float *dsum, int B, int T, int NH) {
-    const int BH = B * NH, nt = (T + 31) / 32;
-    const long long waves = (long long)BH * nt * (MODE == 0 ? 2 : 1);
+template <int HS, int WPB, int MODE, int MINW>
+void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float *lse,
+                  const float *dsum, int B, int T, int NH) {
+    const int BH = B * NH;
+    const int blocks = grid_blocks(BH, T, 32 * WPB) * (MODE == 0 ? 2 : 1);
     const float scale = 1.0f / sqrtf((float)HS);
-    bmb::launch(flash_bwd_k<HS, WPB, MODE>, dim3((unsigned)((waves + WPB - 1) / WPB)),
-                dim3(WPB * 64), 0, nullptr, dqkv, qkv, dout, lse, dsum, T, NH, BH,
-                scale, scale * LOG2E);
+    const size_t smem = BwdSmem<HS>::BYTES;
+    auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
+    allow_smem(kern, smem);
+    bmb::launch(kern, dim3(blocks), dim3(WPB * 64), smem, nullptr, dqkv, qkv, dout, lse, dsum,
+                T, NH, BH, scale, scale * LOG2E);
 }
 
-template <int HS, int WPB>
-void run_bwd(bool fused, float *dqkv, float *dsum, const float *dout,
-             const float *qkv, const float *out, const float *lse, int B, int T,
-             int NH) {
+template <int HS, int WPB, int MINW>
+void run_bwd(bool fused, float *dqkv, float *dsum, const float *dout, const float *qkv,
+             const float *out, const float *lse, int B, int T, int NH) {
     const long long rows = (long long)B * T * NH;
     const long long threads = rows * (HS / 4);
     bmb::launch(flash_dsum_k<HS>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                 nullptr, dsum, dout, out, T, NH, rows);
     if (fused) {
-        run_bwd_mode<HS, WPB, 0>(dqkv, dout, qkv, lse, dsum, B, T, NH);
+        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
     } else {
-        run_bwd_mode<HS, WPB, 1>(dqkv, dout, qkv, lse, dsum, B, T, NH);
-        run_bwd_mode<HS, WPB, 2>(dqkv, dout, qkv, lse, dsum, B, T, NH);
+        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
+        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
     }
 }
 
@@ -507,16 +762,19 @@ template <int HS>
 bool bwd_hs(int cfg, float *dqkv, float *dsum, const float *dout, const float *qkv,
             const float *out, const float *lse, int B, int T, int NH) {
     const BwdCfg &c = BWD_CFGS[cfg];
-    switch (c.wpb) {
-    case 1: run_bwd<HS, 1>(c.fused, dqkv, dsum, dout, qkv, out, lse, B, T, NH); return true;
-    case 2: run_bwd<HS, 2>(c.fused, dqkv, dsum, dout, qkv, out, lse, B, T, NH); return true;
-    case 4: run_bwd<HS, 4>(c.fused, dqkv, dsum, dout, qkv, out, lse, B, T, NH); return true;
-    default: return false;
+#define BMB_BWD(W, M)                                                              \
+    if (c.wpb == W && c.minw == M) {                                               \
+        run_bwd<HS, W, M>(c.fused, dqkv, dsum, dout, qkv, out, lse, B, T, NH);     \
+        return true;                                                               \
     }
+    BMB_BWD(4, 2)
+    BMB_BWD(2, 2)
+    BMB_BWD(4, 1)
+#undef BMB_BWD
+    return false;
 }
 
-// Shape legality shared by forward and backward: a supported head size and
-// 16-byte aligned rows (every fragment is a run of 128-bit loads).
+// Shape legality shared by forward and backward: a supported head size.
 bool shape_ok(int B, int T, int C, int NH, int &hs) {
     if (B < 0 || T < 0 || NH <= 0 || C <= 0 || C % NH != 0) return false;
     hs = C / NH;
@@ -535,10 +793,11 @@ const char *flash_config_name(int cfg) {
 
 int flash_default_config(void) { return FWD_DEFAULT; }
 
-bool flash_attention_forward_cfg(int cfg, float *out, float *lse,
-                                 const float *qkv, int B, int T, int C, int NH) {
+bool flash_attention_forward_cfg(int cfg, float *out, float *lse, const float *qkv, int B,
+                                 int T, int C, int NH) {
     int hs;
     if (cfg < 0 || cfg >= N_FWD || !shape_ok(B, T, C, NH, hs)) return false;
+    // Every row segment is a run of 128-bit loads and stores.
     if (!aligned16(qkv) || !aligned16(out)) return false;
     if (B == 0 || T == 0) return true;
     switch (hs) {
@@ -549,10 +808,9 @@ bool flash_attention_forward_cfg(int cfg, float *out, float *lse,
     }
 }
 
-void flash_attention_forward(float *out, float *lse, const float *qkv, int B,
-                             int T, int C, int NH) {
-    if (flash_attention_forward_cfg(flash_default_config(), out, lse, qkv, B, T, C, NH))
-        return;
+void flash_attention_forward(float *out, float *lse, const float *qkv, int B, int T, int C,
+                             int NH) {
+    if (flash_attention_forward_cfg(flash_default_config(), out, lse, qkv, B, T, C, NH)) return;
     for (int cfg = 0; cfg < N_FWD; ++cfg)
         if (flash_attention_forward_cfg(cfg, out, lse, qkv, B, T, C, NH)) return;
     fprintf(stderr, "flash: no tile config for head size %d (C=%d, NH=%d)\n",
@@ -568,9 +826,8 @@ const char *flash_bwd_config_name(int cfg) {
 
 int flash_default_bwd_config(void) { return BWD_DEFAULT; }
 
-bool flash_attention_backward_cfg(int cfg, float *dqkv, float *dsum,
-                                  const float *dout, const float *qkv,
-                                  const float *out, const float *lse, int B,
+bool flash_attention_backward_cfg(int cfg, float *dqkv, float *dsum, const float *dout,
+                                  const float *qkv, const float *out, const float *lse, int B,
                                   int T, int C, int NH) {
     int hs;
     if (cfg < 0 || cfg >= N_BWD || !shape_ok(B, T, C, NH, hs)) return false;
@@ -585,15 +842,13 @@ bool flash_attention_backward_cfg(int cfg, float *dqkv, float *dsum,
     }
 }
 
-void flash_attention_backward(float *dqkv, float *dsum, const float *dout,
-                              const float *qkv, const float *out,
-                              const float *lse, int B, int T, int C, int NH) {
-    if (flash_attention_backward_cfg(flash_default_bwd_config(), dqkv, dsum, dout,
-                                     qkv, out, lse, B, T, C, NH))
+void flash_attention_backward(float *dqkv, float *dsum, const float *dout, const float *qkv,
+                              const float *out, const float *lse, int B, int T, int C, int NH) {
+    if (flash_attention_backward_cfg(flash_default_bwd_config(), dqkv, dsum, dout, qkv, out,
+                                     lse, B, T, C, NH))
         return;
     for (int cfg = 0; cfg < N_BWD; ++cfg)
-        if (flash_attention_backward_cfg(cfg, dqkv, dsum, dout, qkv, out, lse, B, T,
-                                         C, NH))
+        if (flash_attention_backward_cfg(cfg, dqkv, dsum, dout, qkv, out, lse, B, T, C, NH))
             return;
     fprintf(stderr, "flash: no backward tile config for head size %d (C=%d, NH=%d)\n",
             NH > 0 ? C / NH : -1, C, NH);

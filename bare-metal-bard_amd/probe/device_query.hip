@@ -55,6 +55,21 @@ __global__ __launch_bounds__(THREADS) void mfma_f32_32_k(float *out, float x, in
     out[blockIdx.x * THREADS + threadIdx.x] = s;
 }
 
+// One dependent accumulation chain per wave (each MFMA reads the previous
+// one's result), for the issue rate of back-to-back dependent MFMAs.
+__global__ __launch_bounds__(THREADS) void mfma_f32_chain_k(float *out, float x, int iters) {
+    f32x16 acc;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const float a = x * threadIdx.x, b = x + threadIdx.x;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    }
+    float s = 0.0f;
+    for (int r = 0; r < 16; ++r) s += acc[r];
+    out[blockIdx.x * THREADS + threadIdx.x] = s;
+}
+
 __global__ __launch_bounds__(THREADS) void mfma_f32_16_k(float *out, float x, int iters) {
     f32x4 acc[4];
     for (int j = 0; j < 4; ++j) for (int r = 0; r < 4; ++r) acc[j][r] = 0.0f;
@@ -140,6 +155,13 @@ int main() {
         float ms = time_ms([&] { mfma_f32_32_k<<<blocks, THREADS>>>(out, 1e-3f, iters); }, 5);
         printf("matrix fp32 v_mfma_f32_32x32x2_f32: %.1f TFLOP/s\n",
                4.0 * iters * 32 * 32 * 2 * 2 * waves / ms / 1e9);
+        for (int wps : {1, 2}) {
+            const int cb = cus * wps;
+            ms = time_ms([&] { mfma_f32_chain_k<<<cb, THREADS>>>(out, 1e-3f, iters); }, 5);
+            printf("matrix fp32 32x32x2, one dependent chain per wave, %d wave(s) per SIMD: "
+                   "%.1f TFLOP/s\n", wps,
+                   4.0 * iters * 32 * 32 * 2 * 2 * (double)cb * (THREADS / 64) / ms / 1e9);
+        }
         ms = time_ms([&] { mfma_f32_16_k<<<blocks, THREADS>>>(out, 1e-3f, iters); }, 5);
         printf("matrix fp32 v_mfma_f32_16x16x4_f32: %.1f TFLOP/s\n",
                4.0 * iters * 16 * 16 * 4 * 2 * waves / ms / 1e9);

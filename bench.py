@@ -38,6 +38,9 @@ def parse():
     ap.add_argument("--no-ladder", action="store_true", help="skip ladder stages 1-8, 10")
     ap.add_argument("--only", choices=["sgemm", "flash"], default=None,
                     help="run one workload only (for profiling)")
+    ap.add_argument("--flash-sweep", action="store_true",
+                    help="also time every forward and backward flash config (as the "
+                         "reference's tools/test_flash.cu:198-227,279-319 sweep does)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain 256 MiB device-to-device copy 3 times, the "
                          "known-size reference dispatch for rocprofv3 --pmc FETCH_SIZE / "
@@ -211,6 +214,22 @@ def main():
             "fwd_config": bmb.flash_configs()[bmb.flash_default_config()],
             "bwd_config": bmb.flash_bwd_configs()[bmb.flash_default_bwd_config()],
         }
+        if args.flash_sweep:
+            sweep = {}
+            for i, name in enumerate(bmb.flash_configs()):
+                f = lambda i=i: bmb.flash_forward_cfg(i, out.data_ptr(), lse.data_ptr(),
+                                                      d_qkv.data_ptr(), Bf, T, C, NH)
+                ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+                sweep["fwd %d %s" % (i, name)] = round(fwd_fl / ms_ / 1e9, 2)
+            fwd()
+            for i, name in enumerate(bmb.flash_bwd_configs()):
+                f = lambda i=i: bmb.flash_backward_cfg(
+                    i, dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(), d_qkv.data_ptr(),
+                    out.data_ptr(), lse.data_ptr(), Bf, T, C, NH)
+                ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+                sweep["bwd %d %s" % (i, name)] = round(bwd_fl / ms_ / 1e9, 2)
+            bmb.check("flash sweep")
+            flash["config_sweep_tflops"] = sweep
 
     cpu = None
     cpu_flash = None
