@@ -696,7 +696,7 @@ const BwdCfg BWD_CFGS[] = {
     {"kv128+q128/wg fused lds mfma32", 4, true, 1},
 };
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
-constexpr int BWD_DEFAULT = 0;
+constexpr int BWD_DEFAULT = 2;
 
 int grid_blocks(int BH, int T, int rows_per_block) {
     return BH * ((T + rows_per_block - 1) / rows_per_block);

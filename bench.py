@@ -1,16 +1,28 @@
 #!/usr/bin/env python3
-"""Headline benchmark: fp32 SGEMM at N=4096 and causal flash fwd+bwd at
-B=8, H=12, T=1024, d=64 on one MI355X, through the C-ABI library.
+"""Benchmark of the SGEMM ladder and the fused causal attention on one
+MI355X, through the C-ABI library (bare-metal-bard_amd/lib/libbmb.so).
 
-A "step" is one SGEMM C = A@B + 0.5*C at M=N=K=4096 (
-alpha=1, beta=0.5, C pre-filled, A/B/C from the reference's xorshift fill)
-on the headline kernel (KERNELS id 9, fp32 MFMA). `value` is its GFLOP/s
-(2*N^3 per step). The flash fwd+bwd figure and the other ladder stages are
-reported in the same JSON line. Inputs are resident in HBM before timing;
-each launch is bracketed by HIP events on the null stream, which is the
-stream the library launches on (and torch's current stream).
+A "step" is one SGEMM C = A@B + 0.5*C at M=N=K=4096 (config 2 of the
+baseline: alpha=1, beta=0.5, C pre-filled; A, B, C from the reference's
+xorshift32 fill, src/bench.cu:59-66,226-228) on the headline kernel, KERNELS
+id 9 (fp32 in, fp32 products, fp32 accumulate on v_mfma_f32_32x32x2_f32).
+`value` is its GFLOP/s (2*N^3 per step, src/bench.cu:107-110). Inputs are
+resident in HBM before timing; every launch is bracketed by HIP events on
+the null stream, which is the stream the library launches on and torch's
+current stream, so `roofline.achieved` is the kernel's own average duration.
+
+The same JSON line also carries (none of them is `value`):
+  * config 1: N=1024, alpha=1, beta=0 for the VALU, MFMA and bf16x3 paths;
+  * config 2: the square sweep N in {512 ... 8192} for the same three paths;
+  * the ladder (ids 1-10) at N=4096;
+  * config 3: gemm() at the GPT-2-small training shapes (BT=8192, C=768),
+    forward NT, backward dX NN (beta 0) and dW TN (beta 1);
+  * config 4: flash fwd+bwd at B=8, H=12, T=1024, d=64, with its roofline;
+  * cpu_baseline: the oracle's order-preserving SGEMM and unfused attention
+    on the host's cores (a bounded sample, reported, not a target).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--only sgemm|flash] [--flash-sweep] [--quick]
 """
 import argparse
 import json
@@ -21,11 +33,13 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "bare-metal-bard_amd"))
 
-PEAK_FP32_TFLOPS = 157.3     # MI355X fp32 vector (packed) = fp32 matrix peak
-PEAK_VALU_SCALAR = 78.6      # 64 fp32 FMA/clk/CU without packed math
+PEAK_FP32_TFLOPS = 157.3     # MI355X fp32 vector = fp32 matrix (published)
+PEAK_BF16_TFLOPS = 2500.0    # dense bf16 MFMA (published)
 PEAK_HBM_GBS = 8000.0
 N_SGEMM = 4096
+SWEEP_N = (512, 1000, 1024, 1536, 2048, 4096, 4097, 6144, 8192)
 FLASH = dict(B=8, NH=12, T=1024, hs=64)
+GPT = dict(BT=8192, C=768, V=50257)
 
 
 def parse():
@@ -35,7 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--kernel", type=int, default=9, help="headline KERNELS id")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-ladder", action="store_true", help="skip ladder stages 1-8, 10")
+    ap.add_argument("--no-ladder", action="store_true", help="skip the ladder, sweep and GPT shapes")
+    ap.add_argument("--quick", action="store_true", help="headline SGEMM and flash only")
     ap.add_argument("--only", choices=["sgemm", "flash"], default=None,
                     help="run one workload only (for profiling)")
     ap.add_argument("--flash-sweep", action="store_true",
@@ -71,8 +86,8 @@ def stats(ms):
 
 def load_traffic():
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
-    WRITE_SIZE, scaled by a copy-kernel calibration), committed under
-    profiles/; None until such a measurement exists."""
+    WRITE_SIZE, scaled by a copy-kernel calibration), committed as
+    profiles/traffic.json; {} until such a measurement exists."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
         return {}
@@ -80,15 +95,17 @@ def load_traffic():
         return json.load(f)
 
 
-def cpu_sgemm_baseline(A, B, C0, N):
+def host_threads():
+    n = len(os.sched_getaffinity(0))
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def cpu_sgemm_baseline(O, A, B, C0, N):
     """The oracle's sequential-fmaf SGEMM (order-preserving, vectorised over
-    j, rows split over all host threads) on a row sample of the N=4096 problem
-    sized to ~10 s, scaled to GFLOP/s."""
-    import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    threads = len(os.sched_getaffinity(0))
-    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    j, rows split over the host threads) on a row sample of the N=4096
+    problem sized to about 10 s, scaled to GFLOP/s; plus the literal
+    single-thread loop at config 1's N=1024 on a row sample."""
+    threads = host_threads()
     rows = 64
     t0 = time.perf_counter()
     O.gemm_f32seq(0, 0, rows, N, N, 1.0, A[:rows], B, 0.5, C0[:rows], threads=threads)
@@ -98,28 +115,49 @@ def cpu_sgemm_baseline(A, B, C0, N):
     O.gemm_f32seq(0, 0, rows, N, N, 1.0, A[:rows], B, 0.5, C0[:rows], threads=threads)
     dt = time.perf_counter() - t0
     gf = 2.0 * rows * N * N / dt / 1e9
-    return {"value": round(gf, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "sample": "sequential-fmaf SGEMM (oracle/oracle.c orc_gemm_f32seq_mt), first %d of "
-                      "4096 rows of the N=4096 problem, %.1f s" % (rows, dt)}
-
-
-def cpu_flash_baseline(qkv, dout, B, T, C, NH):
-    """Unfused fp32 causal attention fwd+bwd (src/attention.cu semantics,
-    oracle orc_attn_fwdbwd_f32, OpenMP over heads) on a head sample."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    threads = len(os.sched_getaffinity(0))
-    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
-    nb = 1
+    n1, r1 = 1024, 128
     t0 = time.perf_counter()
-    O.attn_fwdbwd_f32(qkv[:nb], dout[:nb], nb, T, C, NH, threads)
-    dt = time.perf_counter() - t0
+    O.gemm_f32seq(0, 0, r1, n1, n1, 1.0, A[:r1, :n1].copy(), B[:n1, :n1].copy(), 0.0, None,
+                  threads=1)
+    dt1 = time.perf_counter() - t0
+    return {"value": round(gf, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": "sequential-fmaf SGEMM (oracle orc_gemm_f32seq_mt, bit-identical to "
+                      "KERNELS ids 1-8), rows 0-%d of the N=4096 alpha=1 beta=0.5 problem, "
+                      "%.1f s" % (rows - 1, dt),
+            "single_thread_config1": {"value": round(2.0 * r1 * n1 * n1 / dt1 / 1e9, 3),
+                                      "unit": "GFLOP/s", "cores": 1,
+                                      "sample": "rows 0-%d of N=1024 alpha=1 beta=0, %.2f s"
+                                                % (r1 - 1, dt1)}}
+
+
+def cpu_flash_baseline(O, qkv, dout, B, T, C, NH):
+    """Unfused fp32 causal attention fwd+bwd (src/attention.cu semantics,
+    oracle orc_attn_fwdbwd_f32, OpenMP over heads) on the first batches of
+    the config 4 problem, about 10 s of work."""
+    threads = host_threads()
     hs = C // NH
-    pairs = nb * NH * T * (T + 1) / 2
+    nb, done, dt = 1, 0, 0.0
+    while True:
+        t0 = time.perf_counter()
+        O.attn_fwdbwd_f32(qkv[done:done + nb], dout[done:done + nb], nb, T, C, NH, threads)
+        dt += time.perf_counter() - t0
+        done += nb
+        if dt > 10.0 or done >= B:
+            break
+        nb = min(B - done, max(1, int(nb * 2)))
+    pairs = done * NH * T * (T + 1) / 2
     tf = 14.0 * hs * pairs / dt / 1e12  # fwd 4*d*P + bwd 10*d*P useful flops
     return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": "unfused fp32 attention fwd+bwd, batch 0 of 8 (12 heads, T=1024, d=64), "
-                      "%.1f s" % dt}
+            "sample": "unfused fp32 attention fwd+bwd (oracle orc_attn_fwdbwd_f32), batches "
+                      "0-%d of 8 (12 heads, T=1024, d=64), %.1f s" % (done - 1, dt)}
+
+
+def sgemm_fn(bmb, kid):
+    return bmb.find_kernel(kid)["fn"]
+
+
+def gf(flops, ms):
+    return round(flops / ms / 1e6, 1)
 
 
 def main():
@@ -137,7 +175,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     assert torch.cuda.current_stream().cuda_stream == 0, "events must be on the null stream"
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O  # input generators only, outside the timed region
+    import oracle as O  # input generators and the CPU baseline only, outside the timed region
+
+    extras = not (args.quick or args.no_ladder or args.only)
 
     if args.copy_calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
@@ -147,130 +187,196 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    result = {}
+    traffic = load_traffic()
+    line = {"metric": "SGEMM GFLOP/s @N=4096 fp32 (% peak); flash fwd+bwd TFLOP/s @T=1024,d=64",
+            "value": None, "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (xorshift32 1e-3 grid inputs with the seeds of "
+                    "src/bench.cu:226-228; attention q,k,v,dO N(0,1) by Box-Muller)"}
+
     N = N_SGEMM
-    flops = 2.0 * N ** 3
     A = O.fill_xorshift(N * N, 0x12345678).reshape(N, N)
     Bm = O.fill_xorshift(N * N, 0x9ABCDEF0).reshape(N, N)
     C0 = O.fill_xorshift(N * N, 0x0F0F0F0F).reshape(N, N)
-    dA = torch.from_numpy(A).cuda()
-    dB = torch.from_numpy(Bm).cuda()
-    dC = torch.from_numpy(C0).cuda()
-
-    def sg(kid):
-        ent = bmb.find_kernel(kid)
-        fn = ent["fn"]
-        return lambda: fn(N, N, N, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr())
-
-    ladder = {}
     if args.only != "flash":
-        ms = timed(sg(args.kernel), args.steps, args.warmup)
+        smax = max(SWEEP_N) if extras else N
+        dA = torch.from_numpy(O.fill_xorshift(smax * smax, 0x12345678)).cuda()
+        dB = torch.from_numpy(O.fill_xorshift(smax * smax, 0x9ABCDEF0)).cuda()
+        dC = torch.from_numpy(O.fill_xorshift(smax * smax, 0x0F0F0F0F)).cuda()
+        dA[:N * N].copy_(torch.from_numpy(A.reshape(-1)))
+        dB[:N * N].copy_(torch.from_numpy(Bm.reshape(-1)))
+        dC[:N * N].copy_(torch.from_numpy(C0.reshape(-1)))
+
+        def sq(kid, n, alpha=1.0, beta=0.5):
+            fn = sgemm_fn(bmb, kid)
+            return lambda: fn(n, n, n, alpha, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
+
+        flops = 2.0 * N ** 3
+        st = stats(timed(sq(args.kernel, N), args.steps, args.warmup))
         bmb.check("sgemm")
-        st = stats(ms)
-        result["sgemm"] = st
-        if not args.no_ladder and args.only is None:
-            for kid in (8, 10, 7, 6, 5, 4, 3):
-                k_ms = timed(sg(kid), max(3, args.steps // 4), 2)
-                bmb.check("sgemm %d" % kid)
-                ks = stats(k_ms)
-                ladder[bmb.find_kernel(kid)["name"]] = {
-                    "id": kid, "gflops_median": round(flops / ks["median_ms"] / 1e6, 1),
-                    "pct_fp32_peak": round(100 * flops / ks["median_ms"] / 1e9 / PEAK_FP32_TFLOPS, 1)}
-
-    flash = None
-    if args.only != "sgemm":
-        Bf, NH, T, hs = FLASH["B"], FLASH["NH"], FLASH["T"], FLASH["hs"]
-        C = NH * hs
-        qkv = O.fill_normal(Bf * T * 3 * C, 0xBEEF).reshape(Bf, T, 3 * C)
-        dout = O.fill_normal(Bf * T * C, 0xD0D0).reshape(Bf, T, C)
-        d_qkv = torch.from_numpy(qkv).cuda()
-        d_dout = torch.from_numpy(dout).cuda()
-        out = torch.empty(Bf * T * C, device="cuda")
-        lse = torch.empty(Bf * NH * T, device="cuda")
-        dqkv = torch.empty(Bf * T * 3 * C, device="cuda")
-        dsum = torch.empty(Bf * NH * T, device="cuda")
-        fwd = lambda: bmb.flash_forward(out.data_ptr(), lse.data_ptr(), d_qkv.data_ptr(),
-                                        Bf, T, C, NH)
-        bwd = lambda: bmb.flash_backward(dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(),
-                                         d_qkv.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                                         Bf, T, C, NH)
-        fwd()
-        f_ms = timed(fwd, args.steps, args.warmup)
-        b_ms = timed(bwd, args.steps, args.warmup)
-        bmb.check("flash")
-        pairs = Bf * NH * T * (T + 1) / 2
-        fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
-        fs, bs = stats(f_ms), stats(b_ms)
-        tot = fs["avg_ms"] + bs["avg_ms"]
-        flash = {
-            "metric": "flash fwd+bwd TFLOP/s @B=8,H=12,T=1024,d=64 (causal, fp32)",
-            "value": round((fwd_fl + bwd_fl) / tot / 1e9, 2), "unit": "TFLOP/s",
-            "ms_fwd": round(fs["avg_ms"], 4), "ms_bwd": round(bs["avg_ms"], 4),
-            "tflops_fwd": round(fwd_fl / fs["avg_ms"] / 1e9, 2),
-            "tflops_bwd": round(bwd_fl / bs["avg_ms"] / 1e9, 2),
-            "pct_fp32_mfma_peak": round(100 * (fwd_fl + bwd_fl) / tot / 1e9 / PEAK_FP32_TFLOPS, 1),
-            "gflop_algorithmic": round((fwd_fl + bwd_fl) / 1e9, 2),
-            "tflops_ref_accounting": round(4.5 * fwd_fl / tot / 1e9, 2),
-            "fwd_config": bmb.flash_configs()[bmb.flash_default_config()],
-            "bwd_config": bmb.flash_bwd_configs()[bmb.flash_default_bwd_config()],
-        }
-        if args.flash_sweep:
-            sweep = {}
-            for i, name in enumerate(bmb.flash_configs()):
-                f = lambda i=i: bmb.flash_forward_cfg(i, out.data_ptr(), lse.data_ptr(),
-                                                      d_qkv.data_ptr(), Bf, T, C, NH)
-                ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
-                sweep["fwd %d %s" % (i, name)] = round(fwd_fl / ms_ / 1e9, 2)
-            fwd()
-            for i, name in enumerate(bmb.flash_bwd_configs()):
-                f = lambda i=i: bmb.flash_backward_cfg(
-                    i, dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(), d_qkv.data_ptr(),
-                    out.data_ptr(), lse.data_ptr(), Bf, T, C, NH)
-                ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
-                sweep["bwd %d %s" % (i, name)] = round(bwd_fl / ms_ / 1e9, 2)
-            bmb.check("flash sweep")
-            flash["config_sweep_tflops"] = sweep
-
-    cpu = None
-    cpu_flash = None
-    if not args.no_cpu:
-        if args.only != "flash":
-            cpu = cpu_sgemm_baseline(A, Bm, C0, N)
-        if flash is not None:
-            cpu_flash = cpu_flash_baseline(qkv, dout, Bf, T, C, NH)
-            flash["cpu_baseline"] = cpu_flash
-
-    traffic = load_traffic()
-    line = {"metric": "SGEMM GFLOP/s @N=4096 fp32 (% peak); flash fwd+bwd TFLOP/s @T=1024,d=64",
-            "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32", "data": "synthetic (xorshift32 1e-3 grid inputs, seeds of "
-                                    "src/bench.cu:226-228; attention N(0,1) Box-Muller)"}
-    if "sgemm" in result:
-        st = result["sgemm"]
-        gfl = flops / st["avg_ms"] / 1e6
+        g = flops / st["avg_ms"] / 1e6
+        ent = bmb.find_kernel(args.kernel)
+        bytes_alg = 4.0 * (3 * N * N + N * N)  # A, B, C read (beta != 0), C written
         line.update({
-            "value": round(gfl, 1), "ms_per_step": round(st["avg_ms"], 4),
-            "pct_of_peak": round(100 * gfl / 1e3 / PEAK_FP32_TFLOPS, 1),
+            "value": round(g, 1), "ms_per_step": round(st["avg_ms"], 4),
+            "pct_of_peak": round(100 * g / 1e3 / PEAK_FP32_TFLOPS, 1),
             "config": {"workload": "sgemm M=N=K=4096 fp32 row-major alpha=1 beta=0.5, "
-                                   "KERNELS id %d (%s)" % (args.kernel,
-                                                           bmb.find_kernel(args.kernel)["name"]),
-                       "global_batch": 1, "seq_len": None, "parallelism": "single-gpu"},
-            "roofline": {"bound": "mfma", "achieved": round(gfl / 1e3, 2),
+                                   "KERNELS id %d (%s)" % (args.kernel, ent["name"]),
+                       "tol": ent["tol"], "algorithmic_gflop": round(flops / 1e9, 2),
+                       "algorithmic_mb": round(bytes_alg / 1e6, 1)},
+            "roofline": {"bound": "mfma", "achieved": round(g / 1e3, 2),
                          "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(gfl / 1e3 / PEAK_FP32_TFLOPS, 4),
-                         "traffic": traffic.get("sgemm_tensorcore_4096")},
+                         "frac": round(g / 1e3 / PEAK_FP32_TFLOPS, 4),
+                         "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
             "sgemm_timing_ms": {k: round(v, 4) for k, v in st.items()},
         })
-        if ladder:
-            line["ladder"] = ladder
-    else:
-        line.update({"value": None, "ms_per_step": None})
-    if flash is not None:
-        line["flash"] = flash
-    if cpu is not None:
+
+        if extras:
+            # Config 1: N=1024, alpha=1, beta=0.
+            c1 = {}
+            for kid in (8, 9, 10):
+                s1 = stats(timed(sq(kid, 1024, 1.0, 0.0), 20, 5))
+                c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3,
+                                                                          s1["median_ms"])
+            line["config1_n1024_gflops"] = c1
+            # Config 2: square sweep, alpha=1, beta=0.5.
+            sweep = {}
+            for kid in (8, 9, 10):
+                row = {}
+                for n in SWEEP_N:
+                    reps = 10 if n <= 4096 else 5
+                    s2 = stats(timed(sq(kid, n), reps, 2))
+                    row[str(n)] = gf(2.0 * n ** 3, s2["median_ms"])
+                sweep["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = row
+            bmb.check("sgemm sweep")
+            line["config2_sweep_gflops"] = sweep
+            # The ladder at N=4096.
+            ladder = {}
+            for kid in range(1, 11):
+                reps, warm = (2, 1) if kid <= 2 else (5, 2)
+                s3 = stats(timed(sq(kid, N), reps, warm))
+                ladder["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = {
+                    "gflops": gf(flops, s3["median_ms"]),
+                    "pct_fp32_peak": round(100 * flops / s3["median_ms"] / 1e9
+                                           / PEAK_FP32_TFLOPS, 1)}
+            bmb.check("ladder")
+            line["ladder_n4096"] = ladder
+            del dA, dB, dC
+            torch.cuda.empty_cache()
+            line["config3_gpt_gemm_gflops"] = gpt_shapes(bmb, O, torch)
+
+    if args.only != "sgemm":
+        line["flash"] = flash_bench(args, bmb, O, torch, traffic)
+
+    if not args.no_cpu and not args.quick:
+        cpu = {}
+        if args.only != "flash":
+            cpu = cpu_sgemm_baseline(O, A, Bm, C0, N)
+        if args.only != "sgemm":
+            Bf, NH, T, hs = FLASH["B"], FLASH["NH"], FLASH["T"], FLASH["hs"]
+            C = NH * hs
+            qkv = O.fill_normal(Bf * T * 3 * C, 0xBEEF).reshape(Bf, T, 3 * C)
+            dout = O.fill_normal(Bf * T * C, 0xD0D0).reshape(Bf, T, C)
+            fl = cpu_flash_baseline(O, qkv, dout, Bf, T, C, NH)
+            line["flash"]["cpu_baseline"] = fl
+            if not cpu:
+                cpu = fl
         line["cpu_baseline"] = cpu
     print(json.dumps(line))
+
+
+def gpt_shapes(bmb, O, torch):
+    """gemm() at the GPT-2-small training shapes (src/gpt.cu:256-376): the
+    forward is NT (weights stored out x in), the backward dX is NN with
+    beta 0 and dW is TN with beta 1 (accumulate)."""
+    BT, C, V = GPT["BT"], GPT["C"], GPT["V"]
+    layers = {"qkv": (C, 3 * C), "attn_proj": (C, C), "mlp_fc": (C, 4 * C),
+              "mlp_proj": (4 * C, C), "lm_head": (C, V)}
+    res = {}
+    for name, (cin, cout) in layers.items():
+        x = torch.from_numpy(O.fill_normal(BT * max(cin, cout), 11)).cuda()
+        w = torch.from_numpy(O.fill_normal(cout * cin, 12, 0.02)).cuda()
+        y = torch.empty(BT * max(cin, cout), device="cuda")
+        fl = 2.0 * BT * cin * cout
+        # forward y[BT,cout] = x[BT,cin] @ w[cout,cin]^T
+        fwd = lambda: bmb.gemm(False, True, BT, cout, cin, 1.0, x.data_ptr(), w.data_ptr(),
+                               0.0, y.data_ptr())
+        # dX[BT,cin] = dY[BT,cout] @ W[cout,cin]
+        dxf = lambda: bmb.gemm(False, False, BT, cin, cout, 1.0, y.data_ptr(), w.data_ptr(),
+                               0.0, x.data_ptr())
+        # dW[cout,cin] += dY^T[cout,BT] @ X[BT,cin]
+        dwf = lambda: bmb.gemm(True, False, cout, cin, BT, 1.0, y.data_ptr(), x.data_ptr(),
+                               1.0, w.data_ptr())
+        reps = 3 if name == "lm_head" else 10
+        res[name] = {"shape": "%dx%dx%d" % (BT, cout, cin),
+                     "fwd_NT": gf(fl, stats(timed(fwd, reps, 2))["median_ms"]),
+                     "dX_NN": gf(fl, stats(timed(dxf, reps, 2))["median_ms"]),
+                     "dW_TN_beta1": gf(fl, stats(timed(dwf, reps, 2))["median_ms"])}
+        bmb.check("gemm " + name)
+        del x, w, y
+    torch.cuda.empty_cache()
+    return res
+
+
+def flash_bench(args, bmb, O, torch, traffic):
+    Bf, NH, T, hs = FLASH["B"], FLASH["NH"], FLASH["T"], FLASH["hs"]
+    C = NH * hs
+    qkv = O.fill_normal(Bf * T * 3 * C, 0xBEEF).reshape(Bf, T, 3 * C)
+    dout = O.fill_normal(Bf * T * C, 0xD0D0).reshape(Bf, T, C)
+    d_qkv = torch.from_numpy(qkv).cuda()
+    d_dout = torch.from_numpy(dout).cuda()
+    out = torch.empty(Bf * T * C, device="cuda")
+    lse = torch.empty(Bf * NH * T, device="cuda")
+    dqkv = torch.empty(Bf * T * 3 * C, device="cuda")
+    dsum = torch.empty(Bf * NH * T, device="cuda")
+    fwd = lambda: bmb.flash_forward(out.data_ptr(), lse.data_ptr(), d_qkv.data_ptr(),
+                                    Bf, T, C, NH)
+    bwd = lambda: bmb.flash_backward(dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(),
+                                     d_qkv.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                     Bf, T, C, NH)
+    fwd()
+    f_ms = timed(fwd, args.steps, args.warmup)
+    b_ms = timed(bwd, args.steps, args.warmup)
+    bmb.check("flash")
+    pairs = Bf * NH * T * (T + 1) / 2
+    fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
+    fs, bs = stats(f_ms), stats(b_ms)
+    tot = fs["avg_ms"] + bs["avg_ms"]
+    tf = (fwd_fl + bwd_fl) / tot / 1e9
+    flash = {
+        "metric": "flash fwd+bwd TFLOP/s @B=8,H=12,T=1024,d=64 (causal, fp32)",
+        "value": round(tf, 2), "unit": "TFLOP/s",
+        "ms_fwd": round(fs["avg_ms"], 4), "ms_bwd": round(bs["avg_ms"], 4),
+        "ms_fwd_median": round(fs["median_ms"], 4), "ms_bwd_median": round(bs["median_ms"], 4),
+        "tflops_fwd": round(fwd_fl / fs["avg_ms"] / 1e9, 2),
+        "tflops_bwd": round(bwd_fl / bs["avg_ms"] / 1e9, 2),
+        "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_TFLOPS, 1),
+        "gflop_algorithmic": round((fwd_fl + bwd_fl) / 1e9, 2),
+        "tflops_ref_accounting": round(4.5 * fwd_fl / tot / 1e9, 2),
+        "fwd_config": bmb.flash_configs()[bmb.flash_default_config()],
+        "bwd_config": bmb.flash_bwd_configs()[bmb.flash_default_bwd_config()],
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
+                     "traffic": traffic.get("flash_fwd_bwd_b8h12t1024d64")},
+    }
+    if args.flash_sweep:
+        sweep = {}
+        for i, name in enumerate(bmb.flash_configs()):
+            f = lambda i=i: bmb.flash_forward_cfg(i, out.data_ptr(), lse.data_ptr(),
+                                                  d_qkv.data_ptr(), Bf, T, C, NH)
+            ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+            sweep["fwd %d %s" % (i, name)] = round(fwd_fl / ms_ / 1e9, 2)
+        fwd()
+        for i, name in enumerate(bmb.flash_bwd_configs()):
+            f = lambda i=i: bmb.flash_backward_cfg(
+                i, dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(), d_qkv.data_ptr(),
+                out.data_ptr(), lse.data_ptr(), Bf, T, C, NH)
+            ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+            sweep["bwd %d %s" % (i, name)] = round(bwd_fl / ms_ / 1e9, 2)
+        bmb.check("flash sweep")
+        flash["config_sweep_tflops"] = sweep
+    return flash
 
 
 if __name__ == "__main__":
