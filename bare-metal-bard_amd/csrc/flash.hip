@@ -44,8 +44,6 @@
 #include <stdio.h>
 #include <stdlib.h>
 
-#include <mutex>
-
 #include "common.hpp"
 #include "../../include/flash.h"
 #include "launch.hpp"
@@ -119,15 +117,36 @@ struct Tile32 {
             bmb::st4(lds + r * ld + c, v[i]);
         }
     }
-    // Transposed copy: element (r, c) goes to lds[c*ld + r].
-    __device__ __forceinline__ void store_cols(float *lds, int ld, int tid) const {
+};
+
+// The same 32 x HS tile, staged transposed: LDS row d holds column d of the
+// tile (32 floats, row stride ld). Each thread owns runs of 4 consecutive rows
+// of one column: it loads them with four 32-bit loads (the lanes of a wave
+// cover 64 consecutive columns of one row per load, so every load is a
+// coalesced 256-byte access) and writes the run with one 128-bit LDS store;
+// with ld = 36 the 16 lanes of each store phase hit 16 distinct 4-bank groups.
+template <int HS, int NT>
+struct TileT32 {
+    static constexpr int PER_T = 8 * HS / NT;  // (column, 4-row run) pairs per thread
+    static_assert(PER_T >= 1 && (8 * HS) % NT == 0, "tile splits evenly over the threads");
+    float4 v[PER_T];
+
+    __device__ __forceinline__ void load(const float *src, size_t rs, int nrows, int tid) {
 #pragma unroll
         for (int i = 0; i < PER_T; ++i) {
-            const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
-            lds[(c + 0) * ld + r] = v[i].x;
-            lds[(c + 1) * ld + r] = v[i].y;
-            lds[(c + 2) * ld + r] = v[i].z;
-            lds[(c + 3) * ld + r] = v[i].w;
+            const int e = tid + i * NT, c = e % HS, r0 = (e / HS) * 4;
+            const float *p = src + (size_t)r0 * rs + c;
+            v[i].x = r0 + 0 < nrows ? p[0] : 0.0f;
+            v[i].y = r0 + 1 < nrows ? p[rs] : 0.0f;
+            v[i].z = r0 + 2 < nrows ? p[2 * rs] : 0.0f;
+            v[i].w = r0 + 3 < nrows ? p[3 * rs] : 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int ld, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, c = e % HS, r0 = (e / HS) * 4;
+            bmb::st4(lds + c * ld + r0, v[i]);
         }
     }
 };
@@ -208,11 +227,12 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
     const int nkt = (kend + 31) / 32;
     const int my_nkt = active ? (min(T, q0w + 32) + 31) / 32 : 0;
 
-    Tile32<HS, NT> kt, vt;
+    Tile32<HS, NT> kt;
+    TileT32<HS, NT> vt;
     kt.load(base + C, rs, min(32, T), tid);
     vt.load(base + 2 * C, rs, min(32, T), tid);
     kt.store_rows(smem, S::LDK, tid);
-    vt.store_cols(smem + 32 * S::LDK, S::LDV, tid);
+    vt.store(smem + 32 * S::LDK, S::LDV, tid);
     __syncthreads();
 
     for (int t = 0; t < nkt; ++t) {
@@ -281,7 +301,7 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
         if (more) {
             float *nb = smem + ((t + 1) & 1) * S::BUF;
             kt.store_rows(nb, S::LDK, tid);
-            vt.store_cols(nb + 32 * S::LDK, S::LDV, tid);
+            vt.store(nb + 32 * S::LDK, S::LDV, tid);
         }
         __syncthreads();
     }
@@ -384,20 +404,23 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
     const int q_start = kblk * KB;
     const int nqt = (T - q_start + 31) / 32;
     Tile32<HS, NT> qt, ot;
-    float lv = 0.0f;  // staging of lse*log2e (tid < 32) and D (32 <= tid < 64)
+    // Staging of lse (tid < 32, scaled to log2 units when stored) and D
+    // (32 <= tid < 64). Nothing is computed on a loaded value before the
+    // store, so the loads stay in flight across the compute of a tile.
+    float lv = 0.0f;
     auto load_tile = [&](int qb) {
         const int nr = min(32, T - qb);
         qt.load(base + (size_t)qb * rs, rs, nr, tid);
         ot.load(dob + (size_t)qb * C, C, nr, tid);
         if (tid < 64) {
             const int q = qb + (tid & 31);
-            lv = q < T ? (tid < 32 ? lrow[q] * LOG2E : drow[q]) : 0.0f;
+            lv = q < T ? (tid < 32 ? lrow[q] : drow[q]) : 0.0f;
         }
     };
     auto store_tile = [&](float *buf) {
         qt.store_rows(buf, S::LD, tid);
         ot.store_rows(buf + 32 * S::LD, S::LD, tid);
-        if (tid < 64) buf[2 * 32 * S::LD + tid] = lv;
+        if (tid < 64) buf[2 * 32 * S::LD + tid] = tid < 32 ? lv * LOG2E : lv;
     };
     load_tile(q_start);
     store_tile(smem);
@@ -443,7 +466,8 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
                     const int r = 4 * j + i;
                     const int q = qb + res_row(r, hf);
                     const bool live = !edge || (q < T && key < T && key <= q);
-                    p[r] = live ? exp2_hw(s[r] - Lr[i]) : 0.0f;
+                    // exp2(-inf) = 0: masked entries without a branch.
+                    p[r] = exp2_hw(live ? s[r] - Lr[i] : -INFINITY);
                     ds[r] = p[r] * (dp[r] - Dr[i]);
                 }
             }
@@ -562,7 +586,7 @@ __device__ __forceinline__ void bwd_q_block(float *smem, float *__restrict__ dqk
             for (int r = 0; r < 16; ++r) {
                 const int kr = kb + res_row(r, hf);
                 const bool live = !edge || (qv && kr < T && kr <= qi);
-                const float p = live ? exp2_hw(s[r] - L2) : 0.0f;
+                const float p = exp2_hw(live ? s[r] - L2 : -INFINITY);
                 ds[r] = p * (dp[r] - Dq);
             }
             // dQ^T += K^T dS^T: step st contracts over key res_row(st, hf).
@@ -634,21 +658,6 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Kernels whose LDS exceeds the 64 KiB default get their limit raised once
-// per device.
-template <typename K>
-void allow_smem(K kern, size_t bytes) {
-    if (bytes <= 65536) return;
-    static std::once_flag once[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
-    std::call_once(once[dev], [&] {
-        bmb::note_launch_status(hipFuncSetAttribute(
-            reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)bytes));
-    });
-}
-
 int cus_per_xcd() {
     static int cached[64] = {0};
     int dev = 0;
@@ -708,7 +717,7 @@ void run_fwd(float *out, float *lse, const float *qkv, int B, int T, int NH) {
     const float qscale = (1.0f / sqrtf((float)HS)) * LOG2E;
     const size_t smem = FwdSmem<HS>::BYTES;
     auto kern = flash_fwd_k<HS, WPB, SNAKE, MINW>;
-    allow_smem(kern, smem);
+    bmb::allow_smem(kern, smem);
     bmb::launch(kern, dim3(grid_blocks(BH, T, 32 * WPB)), dim3(WPB * 64), smem, nullptr, out,
                 lse, qkv, T, NH, BH, qscale, cus_per_xcd());
 }
@@ -738,7 +747,7 @@ void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float 
     const float scale = 1.0f / sqrtf((float)HS);
     const size_t smem = BwdSmem<HS>::BYTES;
     auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
-    allow_smem(kern, smem);
+    bmb::allow_smem(kern, smem);
     bmb::launch(kern, dim3(blocks), dim3(WPB * 64), smem, nullptr, dqkv, qkv, dout, lse, dsum,
                 T, NH, BH, scale, scale * LOG2E);
 }

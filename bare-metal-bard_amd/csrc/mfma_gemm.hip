@@ -15,7 +15,7 @@
 namespace {
 
 using bmb::MfmaTile;
-using TileL = MfmaTile<256, 256, 8, 2, 4>;   // 512 lanes, 128x64 per wave
+using TileL = MfmaTile<256, 256, 16, 2, 4>;  // 512 lanes, 128x64 per wave
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
 
@@ -29,6 +29,8 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, batch);
+    bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true>, L::SMEM_BYTES);
+    bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false>, L::SMEM_BYTES);
     if (vec)
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,

@@ -25,6 +25,15 @@
 // The +4 pad spreads 16 consecutive rows of a 128-bit read over all 64 banks;
 // the +8 pad puts the two half-waves of a 32-bit read (rows 4 apart) in
 // opposite halves of the banks.
+//
+// Schedule. K is consumed in tiles of BK (a multiple of 16: an even number of
+// 8-k groups) through two LDS stages. Fragments are double-buffered in
+// registers: while the MFMAs of group g run, the LDS reads of group g+1 are in
+// flight. The last group of a tile is issued AFTER the barrier that publishes
+// the next stage, together with the reads of that stage's first group, so the
+// MFMA pipe stays busy across the barrier; the global loads for the stage
+// after next are issued right before the barrier and have a whole tile of
+// MFMAs to land.
 #pragma once
 
 #include "common.hpp"
@@ -41,7 +50,7 @@ struct MfmaTile {
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int FM = WM / 32, FN = WN / 32;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is whole 32x32 MFMA tiles");
-    static_assert(BK % 8 == 0, "BK is a whole number of 8-k groups");
+    static_assert(BK % 16 == 0, "BK is an even number of 8-k groups");
 };
 
 template <bool TA, bool TB, class Tile>
@@ -67,6 +76,10 @@ struct MfmaLayout {
 // Loads one operand chunk (4 floats along the operand's contiguous axis) from
 // global memory, zero filling whatever lies outside [0, rows) x [0, cols).
 // `row` and `col0` index the stored matrix (rows x cols, row-major).
+// VEC: cols % 4 == 0 and a 16-byte aligned base, so an in-range chunk is one
+// aligned 128-bit load. Otherwise a chunk that lies wholly inside the row is
+// still one 128-bit load (global loads on gfx950 need only dword alignment)
+// and only a chunk straddling the row end falls back to guarded 32-bit loads.
 template <bool VEC>
 __device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols,
                                              int row, int col0) {
@@ -75,11 +88,12 @@ __device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols,
     const float *p = P + (size_t)row * cols + col0;
     if (VEC) {
         if (col0 < cols) v = ld4(p);
+    } else if (col0 + 3 < cols) {
+        __builtin_memcpy(&v, p, sizeof(v));
     } else {
         if (col0 + 0 < cols) v.x = p[0];
         if (col0 + 1 < cols) v.y = p[1];
         if (col0 + 2 < cols) v.z = p[2];
-        if (col0 + 3 < cols) v.w = p[3];
     }
     return v;
 }
@@ -173,12 +187,26 @@ struct MfmaGemm {
         }
     }
 
+    __device__ static __forceinline__ void mma(const float (&fa)[FM][4],
+                                               const float (&fb)[FN][4],
+                                               f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    acc[fi][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fi][j], fb[fn][j],
+                                                                       acc[fi][fn], 0, 0, 0);
+    }
+
     // One output tile (m0, n0) of one problem. smem holds two stages.
     __device__ static __forceinline__ void run(int M, int N, int K, float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B,
                                                float beta, float *C, int m0,
                                                int n0, float *smem) {
+        constexpr int G = BK / 8;  // 8-k groups per tile (even)
         const int tid = threadIdx.x;
         const int wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tile::WAVES_N) * WM;
@@ -193,38 +221,36 @@ struct MfmaGemm {
                 for (int r = 0; r < 16; ++r) acc[fi][fn][r] = 0.0f;
 
         const int nkt = (K + BK - 1) / BK;
-        Regs g;
         if (nkt > 0) {
+            Regs g;
             load(g, A, B, M, N, K, m0, n0, 0, tid);
             store(g, smem, smem + L::A_SZ, tid);
-        }
-        __syncthreads();
-
-        for (int kt = 0; kt < nkt; ++kt) {
-            float *stage = smem + (kt & 1) * L::STAGE;
-            const bool more = kt + 1 < nkt;
-            if (more) load(g, A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
-
-            const float *as = stage, *bs = stage + L::A_SZ;
-#pragma unroll
-            for (int grp = 0; grp < BK / 8; ++grp) {
-                float fa[FM][4], fb[FN][4];
-                fragments(as, bs, grp, wm, wn, lane, fa, fb);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int fi = 0; fi < FM; ++fi)
-#pragma unroll
-                        for (int fn = 0; fn < FN; ++fn)
-                            acc[fi][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                fa[fi][j], fb[fn][j], acc[fi][fn], 0, 0, 0);
-            }
-
-            if (more) {
-                float *next = smem + ((kt + 1) & 1) * L::STAGE;
-                store(g, next, next + L::A_SZ, tid);
-            }
+            if (nkt > 1) load(g, A, B, M, N, K, m0, n0, BK, tid);
             __syncthreads();
+
+            float fa[2][FM][4], fb[2][FN][4];
+            fragments(smem, smem + L::A_SZ, 0, wm, wn, lane, fa[0], fb[0]);
+            for (int kt = 0; kt < nkt; ++kt) {
+                const float *as = smem + (kt & 1) * L::STAGE, *bs = as + L::A_SZ;
+#pragma unroll
+                for (int grp = 0; grp < G; ++grp) {
+                    const int cb = grp & 1;  // G is even: group 0 of every tile is buffer 0
+                    if (grp + 1 < G) {
+                        fragments(as, bs, grp + 1, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
+                    } else {
+                        // Publish the next stage, start the global loads of
+                        // the one after, and read group 0 of the next stage
+                        // while this tile's last MFMAs run.
+                        float *nxt = smem + ((kt + 1) & 1) * L::STAGE;
+                        if (kt + 1 < nkt) store(g, nxt, nxt + L::A_SZ, tid);
+                        if (kt + 2 < nkt) load(g, A, B, M, N, K, m0, n0, (kt + 2) * BK, tid);
+                        __syncthreads();
+                        if (kt + 1 < nkt)
+                            fragments(nxt, nxt + L::A_SZ, 0, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
+                    }
+                    mma(fa[cb], fb[cb], acc);
+                }
+            }
         }
 
         // Epilogue: lanes 0-31 of a register cover 32 consecutive columns, so
