@@ -188,6 +188,67 @@ struct FwdSmem {
     static constexpr size_t BYTES = 2 * (size_t)BUF * sizeof(float);
 };
 
+// One 32-key tile of the forward for this wave's 32 queries: S^T = K Q^T in
+// log2 units, online-softmax update of (m, l, O^T), O^T += V^T P^T.
+// ks: K tile rows (stride LDK); vs: V^T rows (stride LDV). MASK: keys past
+// the query (diagonal tile) or past T (ragged tile) get -inf.
+template <int HS, bool MASK>
+__device__ __forceinline__ void fwd_tile(const float *ks, const float *vs, const float (&qf)[HS / 2],
+                                         f32x16 (&o)[HS / 32], float &m, float &l, int kb,
+                                         int qi, int T, int l32, int hf) {
+    constexpr int HH = HS / 2, DT = HS / 32;
+    using S = FwdSmem<HS>;
+    f32x16 s = zero16();
+    const float *krow = ks + l32 * S::LDK + hf * HH;
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        const float4 kv = bmb::ld4(krow + j);
+        s = mfma(kv.x, qf[j + 0], s);
+        s = mfma(kv.y, qf[j + 1], s);
+        s = mfma(kv.z, qf[j + 2], s);
+        s = mfma(kv.w, qf[j + 3], s);
+    }
+    if (MASK) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kb + res_row(r, hf);
+            s[r] = ((key > qi) | (key >= T)) ? -INFINITY : s[r];
+        }
+    }
+    float mb = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+    const float mn = fmaxf(m, pair_max(mb));  // finite: key 0 is live for every query
+    const float alpha = exp2_hw(m - mn);      // 0 on the first tile
+    float p[16], ls = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        p[r] = exp2_hw(s[r] - mn);
+        ls += p[r];
+    }
+    l = l * alpha + ls;  // this half's keys; halves are combined at the end
+    m = mn;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+
+    // O^T += V^T P^T. Step st pairs key res_row(st, hf) of this half; keys
+    // 8j + 4hf + 0..3 are 4 consecutive floats of a V^T row.
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+        const float *vrow = vs + (d * 32 + l32) * S::LDV + 4 * hf;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 vv = bmb::ld4(vrow + 8 * j);
+            o[d] = mfma(vv.x, p[4 * j + 0], o[d]);
+            o[d] = mfma(vv.y, p[4 * j + 1], o[d]);
+            o[d] = mfma(vv.z, p[4 * j + 2], o[d]);
+            o[d] = mfma(vv.w, p[4 * j + 3], o[d]);
+        }
+    }
+}
+
 template <int HS, int WPB, bool SNAKE, int MINW>
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
 flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__restrict__ qkv,
@@ -245,58 +306,12 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
         }
         if (t < my_nkt) {
             const float *ks = smem + (t & 1) * S::BUF;
-            const float *vs = ks + 32 * S::LDK;
-
-            // S^T = K Q^T, 32 keys x 32 queries, log2 units.
-            f32x16 s = zero16();
-            const float *krow = ks + l32 * S::LDK + hf * HH;
-#pragma unroll
-            for (int j = 0; j < HH; j += 4) {
-                const float4 kv = bmb::ld4(krow + j);
-                s = mfma(kv.x, qf[j + 0], s);
-                s = mfma(kv.y, qf[j + 1], s);
-                s = mfma(kv.z, qf[j + 2], s);
-                s = mfma(kv.w, qf[j + 3], s);
-            }
-            if (kb + 32 > q0w || kb + 32 > T) {  // diagonal or ragged tile
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kb + res_row(r, hf);
-                    if (key > qi || key >= T) s[r] = -INFINITY;
-                }
-            }
-            float mb = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
-            const float mn = fmaxf(m, pair_max(mb));  // finite: key kb is live in tile 0
-            const float alpha = exp2_hw(m - mn);      // 0 on the first tile
-            float p[16], ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                p[r] = exp2_hw(s[r] - mn);
-                ls += p[r];
-            }
-            l = l * alpha + ls;  // this half's keys; halves are combined at the end
-            m = mn;
-#pragma unroll
-            for (int d = 0; d < DT; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-
-            // O^T += V^T P^T. Step st pairs key res_row(st, hf) of this half;
-            // keys 8j + 4hf + 0..3 are 4 consecutive floats of a V^T row.
-#pragma unroll
-            for (int d = 0; d < DT; ++d) {
-                const float *vrow = vs + (d * 32 + l32) * S::LDV + 4 * hf;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 vv = bmb::ld4(vrow + 8 * j);
-                    o[d] = mfma(vv.x, p[4 * j + 0], o[d]);
-                    o[d] = mfma(vv.y, p[4 * j + 1], o[d]);
-                    o[d] = mfma(vv.z, p[4 * j + 2], o[d]);
-                    o[d] = mfma(vv.w, p[4 * j + 3], o[d]);
-                }
-            }
+            // Only the diagonal and a ragged last tile need the mask; each
+            // variant is straight-line code the scheduler can interleave.
+            if (kb + 32 > q0w || kb + 32 > T)
+                fwd_tile<HS, true>(ks, ks + 32 * S::LDK, qf, o, m, l, kb, qi, T, l32, hf);
+            else
+                fwd_tile<HS, false>(ks, ks + 32 * S::LDK, qf, o, m, l, kb, qi, T, l32, hf);
         }
         if (more) {
             float *nb = smem + ((t + 1) & 1) * S::BUF;
@@ -360,6 +375,113 @@ struct BwdSmem {
     static constexpr int BUF = KV_BUF > Q_BUF ? KV_BUF : Q_BUF;
     static constexpr size_t BYTES = 2 * (size_t)BUF * sizeof(float);
 };
+
+// One 32-query tile of the dK/dV pass for this wave's 32 keys.
+// qs: Q rows, then dO rows (stride LD), then lse*log2e and D (32 each).
+// S = Q K^T and dP = dO V^T (lane holds key l32, register r holds query
+// qb + res_row(r, hf)); P = exp2(S - lse), dS = P (dP - D); then
+// dV += P^T dO and dK += dS^T Q, whose step st contracts over query
+// res_row(st, hf). MASK: entries with key > query or query >= T are 0.
+template <int HS, bool MASK>
+__device__ __forceinline__ void kv_tile(const float *qs, const float (&kf)[HS / 2],
+                                        const float (&vf)[HS / 2], f32x16 (&dv)[HS / 32],
+                                        f32x16 (&dk)[HS / 32], int qb, int key, int T, int l32,
+                                        int hf) {
+    constexpr int HH = HS / 2, DT = HS / 32;
+    using S = BwdSmem<HS>;
+    const float *os = qs + 32 * S::LD;
+    const float *ls = qs + 2 * 32 * S::LD;
+    f32x16 s = zero16(), dp = zero16();
+    const float *qrow = qs + l32 * S::LD + hf * HH;
+    const float *orow = os + l32 * S::LD + hf * HH;
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        const float4 qa = bmb::ld4(qrow + j), da = bmb::ld4(orow + j);
+        s = mfma(qa.x, kf[j + 0], s);
+        dp = mfma(da.x, vf[j + 0], dp);
+        s = mfma(qa.y, kf[j + 1], s);
+        dp = mfma(da.y, vf[j + 1], dp);
+        s = mfma(qa.z, kf[j + 2], s);
+        dp = mfma(da.z, vf[j + 2], dp);
+        s = mfma(qa.w, kf[j + 3], s);
+        dp = mfma(da.w, vf[j + 3], dp);
+    }
+    float p[16], ds[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 L4 = bmb::ld4(ls + 8 * j + 4 * hf);
+        const float4 D4 = bmb::ld4(ls + 32 + 8 * j + 4 * hf);
+        const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
+        const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * j + i;
+            float x = s[r] - Lr[i];
+            if (MASK) {
+                const int q = qb + res_row(r, hf);
+                x = ((key > q) | (q >= T)) ? -INFINITY : x;  // exp2(-inf) = 0
+            }
+            p[r] = exp2_hw(x);
+            ds[r] = p[r] * (dp[r] - Dr[i]);
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+        const int qr = res_row(st, hf);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            dv[d] = mfma(p[st], os[qr * S::LD + d * 32 + l32], dv[d]);
+            dk[d] = mfma(ds[st], qs[qr * S::LD + d * 32 + l32], dk[d]);
+        }
+    }
+}
+
+// One 32-key tile of the dQ pass for this wave's 32 queries. ks: K rows, then
+// V rows (stride LD). S^T = K Q^T and dP^T = V dO^T (lane holds query l32,
+// register r holds key kb + res_row(r, hf)); dS^T = P^T (dP^T - D);
+// dQ^T += K^T dS^T, whose step st contracts over key res_row(st, hf).
+// MASK: entries with key > query, key >= T or query >= T are 0.
+template <int HS, bool MASK>
+__device__ __forceinline__ void q_tile(const float *ks, const float (&qf)[HS / 2],
+                                       const float (&df)[HS / 2], float L2, float Dq,
+                                       f32x16 (&dq)[HS / 32], int kb, int qi, bool qv, int T,
+                                       int l32, int hf) {
+    constexpr int HH = HS / 2, DT = HS / 32;
+    using S = BwdSmem<HS>;
+    const float *vs = ks + 32 * S::LD;
+    f32x16 s = zero16(), dp = zero16();
+    const float *krow = ks + l32 * S::LD + hf * HH;
+    const float *vrow = vs + l32 * S::LD + hf * HH;
+#pragma unroll
+    for (int j = 0; j < HH; j += 4) {
+        const float4 ka = bmb::ld4(krow + j), va = bmb::ld4(vrow + j);
+        s = mfma(ka.x, qf[j + 0], s);
+        dp = mfma(va.x, df[j + 0], dp);
+        s = mfma(ka.y, qf[j + 1], s);
+        dp = mfma(va.y, df[j + 1], dp);
+        s = mfma(ka.z, qf[j + 2], s);
+        dp = mfma(va.z, df[j + 2], dp);
+        s = mfma(ka.w, qf[j + 3], s);
+        dp = mfma(va.w, df[j + 3], dp);
+    }
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float x = s[r] - L2;
+        if (MASK) {
+            const int kr = kb + res_row(r, hf);
+            x = ((kr > qi) | (kr >= T) | !qv) ? -INFINITY : x;
+        }
+        ds[r] = exp2_hw(x) * (dp[r] - Dq);
+    }
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+        const int kr = res_row(st, hf);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+            dq[d] = mfma(ks[kr * S::LD + d * 32 + l32], ds[st], dq[d]);
+    }
+}
 
 // dK, dV for the WPB*32 keys of key block kblk of head bh.
 template <int HS, int WPB>
@@ -432,57 +554,10 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
         if (more) load_tile(qb + 32);
         if (active && t >= wave) {
             const float *qs = smem + (t & 1) * S::BUF;
-            const float *os = qs + 32 * S::LD;
-            const float *ls = qs + 2 * 32 * S::LD;
-
-            // S = Q K^T and dP = dO V^T: 32 queries x 32 keys; lane holds key
-            // l32, register r holds query qb + res_row(r, hf).
-            f32x16 s = zero16(), dp = zero16();
-            const float *qrow = qs + l32 * S::LD + hf * HH;
-            const float *orow = os + l32 * S::LD + hf * HH;
-#pragma unroll
-            for (int j = 0; j < HH; j += 4) {
-                const float4 qa = bmb::ld4(qrow + j), da = bmb::ld4(orow + j);
-                s = mfma(qa.x, kf[j + 0], s);
-                dp = mfma(da.x, vf[j + 0], dp);
-                s = mfma(qa.y, kf[j + 1], s);
-                dp = mfma(da.y, vf[j + 1], dp);
-                s = mfma(qa.z, kf[j + 2], s);
-                dp = mfma(da.z, vf[j + 2], dp);
-                s = mfma(qa.w, kf[j + 3], s);
-                dp = mfma(da.w, vf[j + 3], dp);
-            }
-
-            const bool edge = qb == k0w || qb + 32 > T || k0w + 32 > T;
-            float p[16], ds[16];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 L4 = bmb::ld4(ls + 8 * j + 4 * hf);
-                const float4 D4 = bmb::ld4(ls + 32 + 8 * j + 4 * hf);
-                const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
-                const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * j + i;
-                    const int q = qb + res_row(r, hf);
-                    const bool live = !edge || (q < T && key < T && key <= q);
-                    // exp2(-inf) = 0: masked entries without a branch.
-                    p[r] = exp2_hw(live ? s[r] - Lr[i] : -INFINITY);
-                    ds[r] = p[r] * (dp[r] - Dr[i]);
-                }
-            }
-
-            // dV += P^T dO, dK += dS^T Q: step st contracts over query
-            // res_row(st, hf); B operands are those rows of dO and Q.
-#pragma unroll
-            for (int st = 0; st < 16; ++st) {
-                const int qr = res_row(st, hf);
-#pragma unroll
-                for (int d = 0; d < DT; ++d) {
-                    dv[d] = mfma(p[st], os[qr * S::LD + d * 32 + l32], dv[d]);
-                    dk[d] = mfma(ds[st], qs[qr * S::LD + d * 32 + l32], dk[d]);
-                }
-            }
+            if (qb == k0w || qb + 32 > T || k0w + 32 > T)  // diagonal or ragged
+                kv_tile<HS, true>(qs, kf, vf, dv, dk, qb, key, T, l32, hf);
+            else
+                kv_tile<HS, false>(qs, kf, vf, dv, dk, qb, key, T, l32, hf);
         }
         if (more) store_tile(smem + ((t + 1) & 1) * S::BUF);
         __syncthreads();
@@ -562,41 +637,10 @@ __device__ __forceinline__ void bwd_q_block(float *smem, float *__restrict__ dqk
         }
         if (t < my_nkt) {
             const float *ks = smem + (t & 1) * S::BUF;
-            const float *vs = ks + 32 * S::LD;
-            // S^T = K Q^T, dP^T = V dO^T: lane holds query l32, register r
-            // holds key kb + res_row(r, hf).
-            f32x16 s = zero16(), dp = zero16();
-            const float *krow = ks + l32 * S::LD + hf * HH;
-            const float *vrow = vs + l32 * S::LD + hf * HH;
-#pragma unroll
-            for (int j = 0; j < HH; j += 4) {
-                const float4 ka = bmb::ld4(krow + j), va = bmb::ld4(vrow + j);
-                s = mfma(ka.x, qf[j + 0], s);
-                dp = mfma(va.x, df[j + 0], dp);
-                s = mfma(ka.y, qf[j + 1], s);
-                dp = mfma(va.y, df[j + 1], dp);
-                s = mfma(ka.z, qf[j + 2], s);
-                dp = mfma(va.z, df[j + 2], dp);
-                s = mfma(ka.w, qf[j + 3], s);
-                dp = mfma(va.w, df[j + 3], dp);
-            }
-            const bool edge = kb + 32 > q0w || kb + 32 > T;
-            float ds[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int kr = kb + res_row(r, hf);
-                const bool live = !edge || (qv && kr < T && kr <= qi);
-                const float p = exp2_hw(live ? s[r] - L2 : -INFINITY);
-                ds[r] = p * (dp[r] - Dq);
-            }
-            // dQ^T += K^T dS^T: step st contracts over key res_row(st, hf).
-#pragma unroll
-            for (int st = 0; st < 16; ++st) {
-                const int kr = res_row(st, hf);
-#pragma unroll
-                for (int d = 0; d < DT; ++d)
-                    dq[d] = mfma(ks[kr * S::LD + d * 32 + l32], ds[st], dq[d]);
-            }
+            if (kb + 32 > q0w || kb + 32 > T)  // diagonal or ragged
+                q_tile<HS, true>(ks, qf, df, L2, Dq, dq, kb, qi, qv, T, l32, hf);
+            else
+                q_tile<HS, false>(ks, qf, df, L2, Dq, dq, kb, qi, qv, T, l32, hf);
         }
         if (more) {
             float *nb = smem + ((t + 1) & 1) * S::BUF;
