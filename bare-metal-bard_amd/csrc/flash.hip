@@ -44,6 +44,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "../../include/flash.h"
 #include "launch.hpp"
@@ -386,7 +388,7 @@ template <int HS, bool MASK>
 __device__ __forceinline__ void kv_tile(const float *qs, const float (&kf)[HS / 2],
                                         const float (&vf)[HS / 2], f32x16 (&dv)[HS / 32],
                                         f32x16 (&dk)[HS / 32], int qb, int key, int T, int l32,
-                                        int hf) {
+                                        int hf, float *__restrict__ ds_out) {
     constexpr int HH = HS / 2, DT = HS / 32;
     using S = BwdSmem<HS>;
     const float *os = qs + 32 * S::LD;
@@ -424,6 +426,12 @@ __device__ __forceinline__ void kv_tile(const float *qs, const float (&kf)[HS / 
             p[r] = exp2_hw(x);
             ds[r] = p[r] * (dp[r] - Dr[i]);
         }
+    }
+    // dS tile for the dQ pass, row-major [query][key]: each half-wave stores
+    // 32 consecutive keys of one query row per instruction.
+    if (ds_out != nullptr) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ds_out[res_row(r, hf) * 32 + l32] = ds[r];
     }
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
@@ -483,14 +491,105 @@ __device__ __forceinline__ void q_tile(const float *ks, const float (&qf)[HS / 2
     }
 }
 
+// dS workspace layout: per head, the 32x32 tiles (query tile qt, key tile
+// kt <= qt) of the causal lower triangle, tile (qt, kt) at index
+// qt(qt+1)/2 + kt, each row-major [query][key].
+__host__ __device__ __forceinline__ size_t ds_tiles_per_head(int T) {
+    const size_t n = (size_t)(T + 31) / 32;
+    return n * (n + 1) / 2;
+}
+__device__ __forceinline__ float *ds_tile(float *ws, int bh, int T, int qt, int kt) {
+    return ws + ((size_t)bh * ds_tiles_per_head(T) + (size_t)qt * (qt + 1) / 2 + kt) * 1024;
+}
+
+// dQ for the WPB*32 queries of query block qblk of head bh from the stored
+// dS tiles: dQ = scale * dS K. The workgroup stages each 32-key K tile in LDS
+// once; wave w multiplies its own dS tile (A operand: lane holds query l32
+// and keys 16*hf + 0..15, read as four 128-bit loads) by it (B operand: K
+// rows 16*hf + st). The result D[query][dim] leaves lane l with dim
+// d*32 + l32 of query rows res_row(r, hf).
+template <int HS, int WPB>
+__device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restrict__ dqkv,
+                                                     const float *__restrict__ qkv,
+                                                     const float *__restrict__ ws, int T,
+                                                     int NH, int qblk, int bh, float scale) {
+    constexpr int NT = WPB * 64, DT = HS / 32;
+    using S = BwdSmem<HS>;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int b = bh / NH, h = bh % NH, C = NH * HS;
+    const size_t rs = 3 * (size_t)C;
+    const float *base = qkv + (size_t)b * T * rs + h * HS;
+
+    const int qtw = qblk * WPB + wave, q0w = qtw * 32;
+    const bool active = q0w < T;
+    const int ntiles = (T + 31) / 32;
+    const int nkt = min(ntiles, qblk * WPB + WPB);  // up to the last wave's diagonal
+    const int my_nkt = active ? qtw + 1 : 0;
+
+    f32x16 dq[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) dq[d] = zero16();
+
+    const float *wsrow = ws + ((size_t)bh * ds_tiles_per_head(T) +
+                               (size_t)qtw * (qtw + 1) / 2) * 1024 + l32 * 32 + 16 * hf;
+    float4 cur[4], nxt[4];
+    if (my_nkt > 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = bmb::ld4(wsrow + 4 * i);
+    }
+    Tile32<HS, NT> kt;
+    kt.load(base + C, rs, min(32, T), tid);
+    kt.store_rows(smem, S::LD, tid);
+    __syncthreads();
+
+    for (int t = 0; t < nkt; ++t) {
+        const bool more = t + 1 < nkt;
+        if (more) kt.load(base + (size_t)(32 * t + 32) * rs + C, rs, min(32, T - 32 * t - 32), tid);
+        if (t + 1 < my_nkt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nxt[i] = bmb::ld4(wsrow + (size_t)(t + 1) * 1024 + 4 * i);
+        }
+        if (t < my_nkt) {
+            const float *ks = smem + (t & 1) * S::BUF;
+            const float a[16] = {cur[0].x, cur[0].y, cur[0].z, cur[0].w,
+                                 cur[1].x, cur[1].y, cur[1].z, cur[1].w,
+                                 cur[2].x, cur[2].y, cur[2].z, cur[2].w,
+                                 cur[3].x, cur[3].y, cur[3].z, cur[3].w};
+#pragma unroll
+            for (int st = 0; st < 16; ++st)
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+                    dq[d] = mfma(a[st], ks[(16 * hf + st) * S::LD + d * 32 + l32], dq[d]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+        }
+        if (more) kt.store_rows(smem + ((t + 1) & 1) * S::BUF, S::LD, tid);
+        __syncthreads();
+    }
+
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int q = q0w + res_row(r, hf);
+        if (q >= T) continue;
+        float *dst = dqkv + ((size_t)b * T + q) * rs + h * HS;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) dst[d * 32 + l32] = dq[d][r] * scale;
+    }
+}
+
 // dK, dV for the WPB*32 keys of key block kblk of head bh.
+// ws: when not null, the dS tiles of head bh are stored there for the dQ
+// pass (lower-triangular tile order, see ds_tile()).
 template <int HS, int WPB>
 __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dqkv,
                                              const float *__restrict__ qkv,
                                              const float *__restrict__ dout,
                                              const float *__restrict__ lse,
                                              const float *__restrict__ dsum, int T, int NH,
-                                             int kblk, int bh, float scale, float qscale) {
+                                             int kblk, int bh, float scale, float qscale,
+                                             float *__restrict__ ws) {
     constexpr int NT = WPB * 64, KB = 32 * WPB, HH = HS / 2, DT = HS / 32;
     using S = BwdSmem<HS>;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -554,10 +653,11 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
         if (more) load_tile(qb + 32);
         if (active && t >= wave) {
             const float *qs = smem + (t & 1) * S::BUF;
+            float *dso = ws ? ds_tile(ws, bh, T, qb >> 5, k0w >> 5) : nullptr;
             if (qb == k0w || qb + 32 > T || k0w + 32 > T)  // diagonal or ragged
-                kv_tile<HS, true>(qs, kf, vf, dv, dk, qb, key, T, l32, hf);
+                kv_tile<HS, true>(qs, kf, vf, dv, dk, qb, key, T, l32, hf, dso);
             else
-                kv_tile<HS, false>(qs, kf, vf, dv, dk, qb, key, T, l32, hf);
+                kv_tile<HS, false>(qs, kf, vf, dv, dk, qb, key, T, l32, hf, dso);
         }
         if (more) store_tile(smem + ((t + 1) & 1) * S::BUF);
         __syncthreads();
@@ -663,12 +763,14 @@ __device__ __forceinline__ void bwd_q_block(float *smem, float *__restrict__ dqk
 }
 
 // MODE 0: dK/dV and dQ workgroups interleaved in one launch.
-// MODE 1: dK/dV only.  MODE 2: dQ only.
+// MODE 1: dK/dV only.  MODE 2: dQ only (recomputing S and dP).
+// MODE 3: dK/dV, also storing dS in ws.  MODE 4: dQ from the dS in ws.
 template <int HS, int WPB, int MODE, int MINW>
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
 flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
             const float *__restrict__ dout, const float *__restrict__ lse,
-            const float *__restrict__ dsum, int T, int NH, int BH, float scale, float qscale) {
+            const float *__restrict__ dsum, int T, int NH, int BH, float scale, float qscale,
+            float *__restrict__ ws) {
     extern __shared__ float smem[];
     constexpr int RB = 32 * WPB;
     const int nblk = (T + RB - 1) / RB;
@@ -686,15 +788,19 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
             bid >>= 1;
         }
     } else {
-        role = MODE - 1;
+        role = MODE == 3 ? 0 : MODE == 4 ? 2 : MODE - 1;
     }
     int blk, bh;
     if (role == 0) {
         work_item<false>(bid, BH, nblk, false, 0, blk, bh);
-        bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
-    } else {
+        bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale,
+                              MODE == 3 ? ws : nullptr);
+    } else if (role == 1) {
         work_item<false>(bid, BH, nblk, true, 0, blk, bh);
         bwd_q_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
+    } else {
+        work_item<false>(bid, BH, nblk, true, 0, blk, bh);
+        bwd_dq_from_ds_block<HS, WPB>(smem, dqkv, qkv, ws, T, NH, blk, bh, scale);
     }
 }
 
@@ -735,21 +841,58 @@ const FwdCfg FWD_CFGS[] = {
 constexpr int N_FWD = sizeof(FWD_CFGS) / sizeof(FWD_CFGS[0]);
 constexpr int FWD_DEFAULT = 0;
 
+// Backward configs. fused: dK/dV and dQ workgroups in one launch; ds_ws:
+// the dK/dV pass stores dS in a library-owned workspace and dQ = scale dS K
+// is a separate light pass (5 matmul passes instead of 7).
 struct BwdCfg {
     const char *name;
     int wpb;
     bool fused;
     int minw;
+    bool ds_ws;
 };
 const BwdCfg BWD_CFGS[] = {
-    {"kv128+q128/wg fused lds mfma32 2w/simd", 4, true, 2},
-    {"kv64+q64/wg fused lds mfma32 2w/simd", 2, true, 2},
-    {"kv128/wg then q128/wg lds mfma32 2w/simd", 4, false, 2},
-    {"kv64/wg then q64/wg lds mfma32 2w/simd", 2, false, 2},
-    {"kv128+q128/wg fused lds mfma32", 4, true, 1},
+    {"kv128+q128/wg fused lds mfma32 2w/simd", 4, true, 2, false},
+    {"kv64+q64/wg fused lds mfma32 2w/simd", 2, true, 2, false},
+    {"kv128/wg then q128/wg lds mfma32 2w/simd", 4, false, 2, false},
+    {"kv64/wg then q64/wg lds mfma32 2w/simd", 2, false, 2, false},
+    {"kv128+q128/wg fused lds mfma32", 4, true, 1, false},
+    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32 2w/simd", 4, false, 2, true},
+    {"kv64/wg storing dS, then dQ=dS.K q64/wg, mfma32 2w/simd", 2, false, 2, true},
 };
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
-constexpr int BWD_DEFAULT = 2;
+constexpr int BWD_DEFAULT = 5;
+
+// dS workspace: one buffer per device, grown on demand and kept until the
+// process ends. Growing waits for the device to go idle first, because
+// earlier launches on any stream may still read the old buffer. Calls on one
+// device share the buffer, so backward calls that run concurrently on two
+// streams of one device race on it (the reference's backward runs on the
+// null stream, where launches are serialised).
+float *ds_workspace(size_t bytes) {
+    static std::mutex mu;
+    static float *ptr[64] = {nullptr};
+    static size_t cap[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < bytes) {
+        if (ptr[dev] != nullptr) {
+            if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+            (void)hipFree(ptr[dev]);
+            ptr[dev] = nullptr;
+            cap[dev] = 0;
+        }
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            (void)hipGetLastError();  // clear the allocation failure
+            return nullptr;
+        }
+        ptr[dev] = static_cast<float *>(p);
+        cap[dev] = bytes;
+    }
+    return ptr[dev];
+}
 
 int grid_blocks(int BH, int T, int rows_per_block) {
     return BH * ((T + rows_per_block - 1) / rows_per_block);
@@ -785,7 +928,7 @@ bool fwd_hs(int cfg, float *out, float *lse, const float *qkv, int B, int T, int
 
 template <int HS, int WPB, int MODE, int MINW>
 void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float *lse,
-                  const float *dsum, int B, int T, int NH) {
+                  const float *dsum, int B, int T, int NH, float *ws) {
     const int BH = B * NH;
     const int blocks = grid_blocks(BH, T, 32 * WPB) * (MODE == 0 ? 2 : 1);
     const float scale = 1.0f / sqrtf((float)HS);
@@ -793,22 +936,31 @@ void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float 
     auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
     bmb::allow_smem(kern, smem);
     bmb::launch(kern, dim3(blocks), dim3(WPB * 64), smem, nullptr, dqkv, qkv, dout, lse, dsum,
-                T, NH, BH, scale, scale * LOG2E);
+                T, NH, BH, scale, scale * LOG2E, ws);
 }
 
 template <int HS, int WPB, int MINW>
-void run_bwd(bool fused, float *dqkv, float *dsum, const float *dout, const float *qkv,
+bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const float *qkv,
              const float *out, const float *lse, int B, int T, int NH) {
+    float *ws = nullptr;
+    if (c.ds_ws) {
+        ws = ds_workspace((size_t)B * NH * ds_tiles_per_head(T) * 1024 * sizeof(float));
+        if (ws == nullptr) return false;  // no workspace: the caller tries another config
+    }
     const long long rows = (long long)B * T * NH;
     const long long threads = rows * (HS / 4);
     bmb::launch(flash_dsum_k<HS>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                 nullptr, dsum, dout, out, T, NH, rows);
-    if (fused) {
-        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
+    if (c.ds_ws) {
+        run_bwd_mode<HS, WPB, 3, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws);
+        run_bwd_mode<HS, WPB, 4, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws);
+    } else if (c.fused) {
+        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
     } else {
-        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
-        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH);
+        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
+        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
     }
+    return true;
 }
 
 template <int HS>
@@ -816,10 +968,8 @@ bool bwd_hs(int cfg, float *dqkv, float *dsum, const float *dout, const float *q
             const float *out, const float *lse, int B, int T, int NH) {
     const BwdCfg &c = BWD_CFGS[cfg];
 #define BMB_BWD(W, M)                                                              \
-    if (c.wpb == W && c.minw == M) {                                               \
-        run_bwd<HS, W, M>(c.fused, dqkv, dsum, dout, qkv, out, lse, B, T, NH);     \
-        return true;                                                               \
-    }
+    if (c.wpb == W && c.minw == M)                                                 \
+        return run_bwd<HS, W, M>(c, dqkv, dsum, dout, qkv, out, lse, B, T, NH);
     BMB_BWD(4, 2)
     BMB_BWD(2, 2)
     BMB_BWD(4, 1)
