@@ -531,13 +531,18 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
 #pragma unroll
     for (int d = 0; d < DT; ++d) dq[d] = zero16();
 
+    // dS tiles stream from HBM with little compute per tile, so each wave
+    // keeps the next PF tiles in flight (a ring of registers).
+    constexpr int PF = 3;
     const float *wsrow = ws + ((size_t)bh * ds_tiles_per_head(T) +
                                (size_t)qtw * (qtw + 1) / 2) * 1024 + l32 * 32 + 16 * hf;
-    float4 cur[4], nxt[4];
-    if (my_nkt > 0) {
+    float4 ring[PF][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cur[i] = bmb::ld4(wsrow + 4 * i);
-    }
+    for (int j = 0; j < PF; ++j)
+        if (j < my_nkt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ring[j][i] = bmb::ld4(wsrow + (size_t)j * 1024 + 4 * i);
+        }
     Tile32<HS, NT> kt;
     kt.load(base + C, rs, min(32, T), tid);
     kt.store_rows(smem, S::LD, tid);
@@ -546,23 +551,27 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
     for (int t = 0; t < nkt; ++t) {
         const bool more = t + 1 < nkt;
         if (more) kt.load(base + (size_t)(32 * t + 32) * rs + C, rs, min(32, T - 32 * t - 32), tid);
-        if (t + 1 < my_nkt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) nxt[i] = bmb::ld4(wsrow + (size_t)(t + 1) * 1024 + 4 * i);
-        }
         if (t < my_nkt) {
             const float *ks = smem + (t & 1) * S::BUF;
-            const float a[16] = {cur[0].x, cur[0].y, cur[0].z, cur[0].w,
-                                 cur[1].x, cur[1].y, cur[1].z, cur[1].w,
-                                 cur[2].x, cur[2].y, cur[2].z, cur[2].w,
-                                 cur[3].x, cur[3].y, cur[3].z, cur[3].w};
+            const float a[16] = {ring[0][0].x, ring[0][0].y, ring[0][0].z, ring[0][0].w,
+                                 ring[0][1].x, ring[0][1].y, ring[0][1].z, ring[0][1].w,
+                                 ring[0][2].x, ring[0][2].y, ring[0][2].z, ring[0][2].w,
+                                 ring[0][3].x, ring[0][3].y, ring[0][3].z, ring[0][3].w};
+            // Rotate the ring and start the load of tile t + PF.
+#pragma unroll
+            for (int j = 0; j + 1 < PF; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ring[j][i] = ring[j + 1][i];
+            if (t + PF < my_nkt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    ring[PF - 1][i] = bmb::ld4(wsrow + (size_t)(t + PF) * 1024 + 4 * i);
+            }
 #pragma unroll
             for (int st = 0; st < 16; ++st)
 #pragma unroll
                 for (int d = 0; d < DT; ++d)
                     dq[d] = mfma(a[st], ks[(16 * hf + st) * S::LD + d * 32 + l32], dq[d]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
         }
         if (more) kt.store_rows(smem + ((t + 1) & 1) * S::BUF, S::LD, tid);
         __syncthreads();
