@@ -5,8 +5,8 @@
 // (src/gemm.cu:204-217); batched_gemm() always uses a guarded 64x64 kernel
 // (src/bgemm.cu:88-97). Here one kernel template handles every shape and
 // transpose in-kernel (guarded, zero-filled staging; guarded stores), and the
-// host only picks the tile size from the amount of parallel work and whether
-// 128-bit global loads are legal.
+// host only picks the tile size (pick_tile) and whether every row of the
+// operands is 16-byte aligned.
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
 #include "../../include/kernels.h"
@@ -19,8 +19,34 @@ using TileL = MfmaTile<256, 256, 16, 2, 4>;  // 512 lanes, 128x64 per wave
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
 
-// Enough workgroups to give every one of the 256 CUs at least one.
-constexpr long long FILL = 224;
+// Number of CUs of the current device (256 on MI355X), cached per device.
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+// Tile choice. Measured on MI355X at fp32 (N=4096/8192): the 256x256 tile
+// (8 waves, one workgroup per CU) reaches ~86% of the MFMA peak, 128x128 (4
+// waves, three per CU) ~82% and 64x64 (4 waves, eight per CU) ~78%. The big
+// tiles lose badly when their count leaves a partial round of workgroups
+// (4097^3 on 256x256: 17*17 = 289 tiles = 1.13 rounds, 63 TFLOP/s against
+// 102 on 64x64), and small problems need the small tile to occupy every CU.
+// So a big tile is used only when it fills whole rounds of the machine.
+enum class TileKind { L, M, S };
+TileKind pick_tile(long long tiles_l, long long tiles_m, int cus) {
+    if (tiles_l >= cus && tiles_l % cus == 0) return TileKind::L;
+    if (tiles_m >= 3LL * cus && tiles_m % (3LL * cus) == 0) return TileKind::M;
+    return TileKind::S;
+}
 
 template <bool TA, bool TB, class Tile>
 void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
@@ -57,12 +83,17 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     auto work = [&](int bm, int bn) {
         return (long long)bmb::ceil_div(M, bm) * bmb::ceil_div(N, bn) * batch;
     };
-    if (work(TileL::BM, TileL::BN) >= FILL)
+    switch (pick_tile(work(TileL::BM, TileL::BN), work(TileM::BM, TileM::BN), device_cus())) {
+    case TileKind::L:
         launch_tile<TA, TB, TileL>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
-    else if (work(TileM::BM, TileM::BN) >= FILL)
+        break;
+    case TileKind::M:
         launch_tile<TA, TB, TileM>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
-    else
+        break;
+    case TileKind::S:
         launch_tile<TA, TB, TileS>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        break;
+    }
 }
 
 void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,

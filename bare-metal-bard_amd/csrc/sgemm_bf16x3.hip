@@ -72,6 +72,11 @@ __device__ __forceinline__ Chunk load4(const float *P, int rows, int K,
                 const float4 v = bmb::ld4(p);
                 c.v[0] = v.x; c.v[1] = v.y; c.v[2] = v.z; c.v[3] = v.w;
             }
+        } else if (gk + 3 < K) {
+            // Interior chunk of an unaligned row: one dword-aligned 128-bit load.
+            float4 v;
+            __builtin_memcpy(&v, p, sizeof(v));
+            c.v[0] = v.x; c.v[1] = v.y; c.v[2] = v.z; c.v[3] = v.w;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)

@@ -7,9 +7,11 @@
 // stages 1-7). Split-K, reassociation or MFMA would all break that, which is
 // why this stage stays on the vector ALU.
 //
-// Ceiling. Without packed FP32 (v_pk_fma_f32 is not used by this build) the
-// vector ALU retires 64 fp32 FMAs per clock per CU, i.e. 78.6 TFLOP/s on 256
-// CUs at 2.4 GHz -- half of the 157.3 TFLOP/s packed-vector peak.
+// Ceiling. This build never emits packed fp32 (v_pk_fma_f32). A single wave
+// issues one v_fmac_f32 every 4 clocks, but several waves on one SIMD issue
+// concurrently: a loop of nothing but FMAs reaches ~112 TFLOP/s (71% of the
+// 157.3 TFLOP/s vector peak) with 8 waves per SIMD, which is the practical
+// ceiling of a kernel that also has to read its operands from LDS.
 //
 // Structure.
 //   * 256 lanes = 4 wave64 per workgroup, 128x128 output tile, BK = 16.
@@ -22,8 +24,10 @@
 //   * Double-buffered LDS with the next tile prefetched into registers while
 //     the current one is consumed: one barrier per BK chunk.
 //   * Ragged M, N, K are handled in-kernel: guarded, zero-filled loads and
-//     guarded stores. There is no fallback kernel. VEC selects 128-bit global
-//     access when K % 4 == 0, N % 4 == 0 and the pointers are 16-byte aligned.
+//     guarded stores. There is no fallback kernel. VEC selects aligned 128-bit
+//     global access when K % 4 == 0, N % 4 == 0 and the pointers are 16-byte
+//     aligned; otherwise interior chunks still use dword-aligned 128-bit loads
+//     and only a chunk that straddles a row end uses 32-bit loads.
 //   * Workgroup ids are remapped so the tiles one XCD runs share panels.
 #include "common.hpp"
 #include "../../include/kernels.h"
@@ -61,6 +65,12 @@ __device__ __forceinline__ void load_tile(Prefetch &p, const float *A,
             if (gm < M && gk < K) v = bmb::ld4(&A[(size_t)gm * K + gk]);
             p.a[r * 4 + 0] = v.x; p.a[r * 4 + 1] = v.y;
             p.a[r * 4 + 2] = v.z; p.a[r * 4 + 3] = v.w;
+        } else if (gm < M && gk + 3 < K) {
+            // Interior chunk of an unaligned row: one dword-aligned 128-bit load.
+            float4 v;
+            __builtin_memcpy(&v, &A[(size_t)gm * K + gk], sizeof(v));
+            p.a[r * 4 + 0] = v.x; p.a[r * 4 + 1] = v.y;
+            p.a[r * 4 + 2] = v.z; p.a[r * 4 + 3] = v.w;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -76,6 +86,11 @@ __device__ __forceinline__ void load_tile(Prefetch &p, const float *A,
         if (VEC) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (gk < K && gn < N) v = bmb::ld4(&B[(size_t)gk * N + gn]);
+            p.b[r * 4 + 0] = v.x; p.b[r * 4 + 1] = v.y;
+            p.b[r * 4 + 2] = v.z; p.b[r * 4 + 3] = v.w;
+        } else if (gk < K && gn + 3 < N) {
+            float4 v;
+            __builtin_memcpy(&v, &B[(size_t)gk * N + gn], sizeof(v));
             p.b[r * 4 + 0] = v.x; p.b[r * 4 + 1] = v.y;
             p.b[r * 4 + 2] = v.z; p.b[r * 4 + 3] = v.w;
         } else {
