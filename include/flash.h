@@ -11,6 +11,15 @@
  *   dsum (B, NH, T)   backward scratch: rowsum(dout * out)
  * scale = 1/sqrt(hs). The T x T score matrix is never materialised. Launches
  * go to the null stream. Supported head sizes: 32, 64, 128.
+ *
+ * Memory: the default backward config stores the causal 32x32 tiles of dS
+ * (fp32, 4 KiB each, B*NH*n(n+1)/2 of them with n = ceil(T/32)) in a
+ * library-owned per-device workspace, allocated on first use, grown on
+ * demand and kept until the process ends. If it cannot be allocated the
+ * backward falls back to a config that recomputes S and dP instead and
+ * allocates nothing; flash_attention_backward_cfg can select such a config
+ * directly. Concurrent backward calls on two streams of one device share the
+ * workspace and must be serialised.
  */
 #ifndef BMB_FLASH_H
 #define BMB_FLASH_H
