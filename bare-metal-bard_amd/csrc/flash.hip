@@ -44,7 +44,9 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "common.hpp"
 #include "../../include/flash.h"
@@ -178,6 +180,32 @@ __device__ __forceinline__ void work_item(int bid, int BH, int nblk, bool longes
         bh = bid % BH;
     }
     blk = longest_hi ? nblk - 1 - rank : rank;
+}
+
+// Per-head work list of a backward pass, built on the host and passed by
+// value: item i streams tiles [t0[i], t1[i]) of block blk[i]; split[i] marks
+// one of the two halves of a long block, whose results are added atomically
+// into rows zeroed beforehand (exactly two addends onto zero, so the sum does
+// not depend on their order). Items are listed longest first.
+constexpr int MAX_ITEMS = 192;
+struct Items {
+    int n;
+    unsigned short blk[MAX_ITEMS], t0[MAX_ITEMS], t1[MAX_ITEMS];
+    unsigned char split[MAX_ITEMS];
+};
+
+// Item and head of workgroup `bid`: XCD-aware as work_item, ranks taken from
+// the longest-first list.
+__device__ __forceinline__ void table_item(int bid, int BH, const Items &it, int &item,
+                                           int &bh) {
+    if (BH % NXCD == 0) {
+        const int xcd = bid % NXCD, w = bid / NXCD, hpx = BH / NXCD;
+        item = w / hpx;
+        bh = (w % hpx) * NXCD + xcd;
+    } else {
+        item = bid / BH;
+        bh = bid % BH;
+    }
 }
 
 // ------------------------------------------------------------------ forward
@@ -343,11 +371,17 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
 // D[b,h,t] = sum_i dO[b,t,h*hs+i] * O[b,t,h*hs+i] (src/flash.cu:471-487).
 // HS/4 lanes per row, one float4 each, reduced with cross-lane xor shuffles.
 // Rows are walked in (b, h, t) order so that the D writes are contiguous.
+// It also zeroes the dK/dV rows of key blocks (of `blk_rows` rows) whose bit
+// is set in kv_zero, and the dQ rows of query blocks set in q_zero, in dqkv:
+// the halves of a split backward item accumulate into them.
 template <int HS>
 __global__ __launch_bounds__(256) void flash_dsum_k(float *__restrict__ dsum,
                                                     const float *__restrict__ dout,
                                                     const float *__restrict__ out,
-                                                    int T, int NH, long long rows) {
+                                                    int T, int NH, long long rows,
+                                                    float *__restrict__ dqkv, int blk_rows,
+                                                    unsigned long long kv_zero,
+                                                    unsigned long long q_zero) {
     constexpr int LPR = HS / 4;  // lanes per row
     const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long row = gid / LPR;  // row = (b*NH + h)*T + t
@@ -365,6 +399,20 @@ __global__ __launch_bounds__(256) void flash_dsum_k(float *__restrict__ dsum,
 #pragma unroll
     for (int w = 1; w < LPR; w <<= 1) s += __shfl_xor(s, w);
     if (row < rows && sub == 0) dsum[row] = s;
+    if (row < rows && (kv_zero | q_zero) != 0) {
+        const int t = (int)(row % T);
+        const long long bh = row / T;
+        const int h = (int)(bh % NH);
+        const long long b = bh / NH;
+        const int blk = t / blk_rows;
+        const size_t C = (size_t)NH * HS;
+        float *r = dqkv + ((size_t)b * T + t) * 3 * C + (size_t)h * HS + sub * 4;
+        if (blk < 64 && ((q_zero >> blk) & 1)) bmb::st4(r, zero4());
+        if (blk < 64 && ((kv_zero >> blk) & 1)) {
+            bmb::st4(r + C, zero4());
+            bmb::st4(r + 2 * C, zero4());
+        }
+    }
 }
 
 template <int HS>
@@ -512,7 +560,8 @@ template <int HS, int WPB>
 __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restrict__ dqkv,
                                                      const float *__restrict__ qkv,
                                                      const float *__restrict__ ws, int T,
-                                                     int NH, int qblk, int bh, float scale) {
+                                                     int NH, int qblk, int bh, float scale,
+                                                     int tk0, int tk1, bool accumulate) {
     constexpr int NT = WPB * 64, DT = HS / 32;
     using S = BwdSmem<HS>;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -523,9 +572,9 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
 
     const int qtw = qblk * WPB + wave, q0w = qtw * 32;
     const bool active = q0w < T;
-    const int ntiles = (T + 31) / 32;
-    const int nkt = min(ntiles, qblk * WPB + WPB);  // up to the last wave's diagonal
-    const int my_nkt = active ? qtw + 1 : 0;
+    // Key tiles [tk0, tk1), each wave up to its diagonal.
+    const int nkt = tk1 - tk0;
+    const int my_nkt = active ? max(0, min(tk1, qtw + 1) - tk0) : 0;
 
     f32x16 dq[DT];
 #pragma unroll
@@ -535,7 +584,7 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
     // keeps the next PF tiles in flight (a ring of registers).
     constexpr int PF = 3;
     const float *wsrow = ws + ((size_t)bh * ds_tiles_per_head(T) +
-                               (size_t)qtw * (qtw + 1) / 2) * 1024 + l32 * 32 + 16 * hf;
+                               (size_t)qtw * (qtw + 1) / 2 + tk0) * 1024 + l32 * 32 + 16 * hf;
     float4 ring[PF][4];
 #pragma unroll
     for (int j = 0; j < PF; ++j)
@@ -544,13 +593,14 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
             for (int i = 0; i < 4; ++i) ring[j][i] = bmb::ld4(wsrow + (size_t)j * 1024 + 4 * i);
         }
     Tile32<HS, NT> kt;
-    kt.load(base + C, rs, min(32, T), tid);
+    kt.load(base + (size_t)tk0 * 32 * rs + C, rs, min(32, T - tk0 * 32), tid);
     kt.store_rows(smem, S::LD, tid);
     __syncthreads();
 
     for (int t = 0; t < nkt; ++t) {
         const bool more = t + 1 < nkt;
-        if (more) kt.load(base + (size_t)(32 * t + 32) * rs + C, rs, min(32, T - 32 * t - 32), tid);
+        const int kn = (tk0 + t + 1) * 32;  // first key of the next tile
+        if (more) kt.load(base + (size_t)kn * rs + C, rs, min(32, T - kn), tid);
         if (t < my_nkt) {
             const float *ks = smem + (t & 1) * S::BUF;
             const float a[16] = {ring[0][0].x, ring[0][0].y, ring[0][0].z, ring[0][0].w,
@@ -583,8 +633,13 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
         const int q = q0w + res_row(r, hf);
         if (q >= T) continue;
         float *dst = dqkv + ((size_t)b * T + q) * rs + h * HS;
+        if (accumulate) {
 #pragma unroll
-        for (int d = 0; d < DT; ++d) dst[d * 32 + l32] = dq[d][r] * scale;
+            for (int d = 0; d < DT; ++d) atomicAdd(dst + d * 32 + l32, dq[d][r] * scale);
+        } else {
+#pragma unroll
+            for (int d = 0; d < DT; ++d) dst[d * 32 + l32] = dq[d][r] * scale;
+        }
     }
 }
 
@@ -598,7 +653,8 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
                                              const float *__restrict__ lse,
                                              const float *__restrict__ dsum, int T, int NH,
                                              int kblk, int bh, float scale, float qscale,
-                                             float *__restrict__ ws) {
+                                             float *__restrict__ ws, int tq0, int tq1,
+                                             bool accumulate) {
     constexpr int NT = WPB * 64, KB = 32 * WPB, HH = HS / 2, DT = HS / 32;
     using S = BwdSmem<HS>;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -630,9 +686,9 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
 #pragma unroll
     for (int d = 0; d < DT; ++d) { dv[d] = zero16(); dk[d] = zero16(); }
 
-    // Query tiles from the workgroup's first key on; wave w starts at tile w.
-    const int q_start = kblk * KB;
-    const int nqt = (T - q_start + 31) / 32;
+    // Query tiles [tq0, tq1); a wave skips the tiles before its diagonal.
+    const int q_start = tq0 * 32;
+    const int nqt = tq1 - tq0;
     Tile32<HS, NT> qt, ot;
     // Staging of lse (tid < 32, scaled to log2 units when stored) and D
     // (32 <= tid < 64). Nothing is computed on a loaded value before the
@@ -660,7 +716,7 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
         const int qb = q_start + 32 * t;
         const bool more = t + 1 < nqt;
         if (more) load_tile(qb + 32);
-        if (active && t >= wave) {
+        if (active && qb >= k0w) {
             const float *qs = smem + (t & 1) * S::BUF;
             float *dso = ws ? ds_tile(ws, bh, T, qb >> 5, k0w >> 5) : nullptr;
             if (qb == k0w || qb + 32 > T || k0w + 32 > T)  // diagonal or ragged
@@ -679,10 +735,18 @@ __device__ __forceinline__ void bwd_kv_block(float *smem, float *__restrict__ dq
         const int kr = k0w + res_row(r, hf);
         if (kr >= T) continue;
         float *dkp = dqkv + ((size_t)b * T + kr) * rs + C + h * HS;
+        if (accumulate) {
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            dkp[d * 32 + l32] = dk[d][r] * scale;
-            dkp[C + d * 32 + l32] = dv[d][r];
+            for (int d = 0; d < DT; ++d) {
+                atomicAdd(dkp + d * 32 + l32, dk[d][r] * scale);
+                atomicAdd(dkp + C + d * 32 + l32, dv[d][r]);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                dkp[d * 32 + l32] = dk[d][r] * scale;
+                dkp[C + d * 32 + l32] = dv[d][r];
+            }
         }
     }
 }
@@ -779,7 +843,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))
 flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
             const float *__restrict__ dout, const float *__restrict__ lse,
             const float *__restrict__ dsum, int T, int NH, int BH, float scale, float qscale,
-            float *__restrict__ ws) {
+            float *__restrict__ ws, const Items items) {
     extern __shared__ float smem[];
     constexpr int RB = 32 * WPB;
     const int nblk = (T + RB - 1) / RB;
@@ -799,17 +863,25 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
     } else {
         role = MODE == 3 ? 0 : MODE == 4 ? 2 : MODE - 1;
     }
+    const int ntiles = (T + 31) / 32;
     int blk, bh;
-    if (role == 0) {
+    if (MODE == 3) {
+        int it;
+        table_item(bid, BH, items, it, bh);
+        bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, items.blk[it], bh,
+                              scale, qscale, ws, items.t0[it], items.t1[it], items.split[it]);
+    } else if (MODE == 4) {
+        int it;
+        table_item(bid, BH, items, it, bh);
+        bwd_dq_from_ds_block<HS, WPB>(smem, dqkv, qkv, ws, T, NH, items.blk[it], bh, scale,
+                                      items.t0[it], items.t1[it], items.split[it]);
+    } else if (role == 0) {
         work_item<false>(bid, BH, nblk, false, 0, blk, bh);
         bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale,
-                              MODE == 3 ? ws : nullptr);
-    } else if (role == 1) {
-        work_item<false>(bid, BH, nblk, true, 0, blk, bh);
-        bwd_q_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
+                              nullptr, blk * WPB, ntiles, false);
     } else {
         work_item<false>(bid, BH, nblk, true, 0, blk, bh);
-        bwd_dq_from_ds_block<HS, WPB>(smem, dqkv, qkv, ws, T, NH, blk, bh, scale);
+        bwd_q_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale);
     }
 }
 
@@ -868,6 +940,7 @@ const BwdCfg BWD_CFGS[] = {
     {"kv128+q128/wg fused lds mfma32", 4, true, 1, false},
     {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32 2w/simd", 4, false, 2, true},
     {"kv64/wg storing dS, then dQ=dS.K q64/wg, mfma32 2w/simd", 2, false, 2, true},
+    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32", 4, false, 1, true},
 };
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
 constexpr int BWD_DEFAULT = 5;
@@ -935,39 +1008,87 @@ bool fwd_hs(int cfg, float *out, float *lse, const float *qkv, int B, int T, int
     return false;
 }
 
+// Per-head work list of the dK/dV pass (kv = true: block = WPB*32 keys,
+// streaming query tiles from its diagonal to the end) or of the dQ-from-dS
+// pass (block = WPB*32 queries, streaming key tiles from 0 to its diagonal).
+// A block much longer than the average (> 1.5x) is split into two halves, so
+// that the longest item no longer sets the length of the whole launch; the
+// bit of a split block is set in *zero_mask. Returns false if T has more
+// blocks than the list (or the zero mask) can hold.
+bool build_items(bool kv, int T, int wpb, Items &it, unsigned long long &zero_mask) {
+    const int ntiles = (T + 31) / 32;
+    const int nblk = (ntiles + wpb - 1) / wpb;
+    zero_mask = 0;
+    if (nblk > MAX_ITEMS) return false;
+    long long total = 0;
+    for (int k = 0; k < nblk; ++k)
+        total += kv ? ntiles - k * wpb : std::min(ntiles, (k + 1) * wpb);
+    struct Item { int blk, t0, t1, split; };
+    std::vector<Item> v;
+    for (int k = 0; k < nblk; ++k) {
+        const int t0 = kv ? k * wpb : 0, t1 = kv ? ntiles : std::min(ntiles, (k + 1) * wpb);
+        const int len = t1 - t0;
+        if (nblk <= 64 && len >= 4 && 2LL * len * nblk > 3 * total &&
+            (int)v.size() + 2 <= MAX_ITEMS) {
+            const int mid = t0 + len / 2;
+            v.push_back({k, t0, mid, 1});
+            v.push_back({k, mid, t1, 1});
+            zero_mask |= 1ULL << k;
+        } else {
+            v.push_back({k, t0, t1, 0});
+        }
+    }
+    std::stable_sort(v.begin(), v.end(),
+                     [](const Item &a, const Item &b) { return a.t1 - a.t0 > b.t1 - b.t0; });
+    it.n = (int)v.size();
+    for (int i = 0; i < it.n; ++i) {
+        it.blk[i] = (unsigned short)v[i].blk;
+        it.t0[i] = (unsigned short)v[i].t0;
+        it.t1[i] = (unsigned short)v[i].t1;
+        it.split[i] = (unsigned char)v[i].split;
+    }
+    return true;
+}
+
 template <int HS, int WPB, int MODE, int MINW>
 void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float *lse,
-                  const float *dsum, int B, int T, int NH, float *ws) {
+                  const float *dsum, int B, int T, int NH, float *ws, const Items &items) {
     const int BH = B * NH;
-    const int blocks = grid_blocks(BH, T, 32 * WPB) * (MODE == 0 ? 2 : 1);
+    const int blocks = (MODE == 3 || MODE == 4) ? BH * items.n
+                                                : grid_blocks(BH, T, 32 * WPB) * (MODE == 0 ? 2 : 1);
     const float scale = 1.0f / sqrtf((float)HS);
     const size_t smem = BwdSmem<HS>::BYTES;
     auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
     bmb::allow_smem(kern, smem);
     bmb::launch(kern, dim3(blocks), dim3(WPB * 64), smem, nullptr, dqkv, qkv, dout, lse, dsum,
-                T, NH, BH, scale, scale * LOG2E, ws);
+                T, NH, BH, scale, scale * LOG2E, ws, items);
 }
 
 template <int HS, int WPB, int MINW>
 bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const float *qkv,
              const float *out, const float *lse, int B, int T, int NH) {
     float *ws = nullptr;
+    Items kv_it, q_it;
+    unsigned long long kv_zero = 0, q_zero = 0;
+    kv_it.n = q_it.n = 0;
     if (c.ds_ws) {
+        if (!build_items(true, T, WPB, kv_it, kv_zero) || !build_items(false, T, WPB, q_it, q_zero))
+            return false;
         ws = ds_workspace((size_t)B * NH * ds_tiles_per_head(T) * 1024 * sizeof(float));
         if (ws == nullptr) return false;  // no workspace: the caller tries another config
     }
     const long long rows = (long long)B * T * NH;
     const long long threads = rows * (HS / 4);
     bmb::launch(flash_dsum_k<HS>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                nullptr, dsum, dout, out, T, NH, rows);
+                nullptr, dsum, dout, out, T, NH, rows, dqkv, 32 * WPB, kv_zero, q_zero);
     if (c.ds_ws) {
-        run_bwd_mode<HS, WPB, 3, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws);
-        run_bwd_mode<HS, WPB, 4, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws);
+        run_bwd_mode<HS, WPB, 3, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, kv_it);
+        run_bwd_mode<HS, WPB, 4, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, q_it);
     } else if (c.fused) {
-        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
+        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
     } else {
-        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
-        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr);
+        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
+        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
     }
     return true;
 }

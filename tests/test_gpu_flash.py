@@ -121,6 +121,16 @@ def test_every_backward_config(gpu, cfg):
     _case(1, 70, 96, 3, 4321, 8765, bcfg=cfg)    # hs 32, B*NH not a multiple of 8
 
 
+@pytest.mark.parametrize("shape", [(2, 500, 256, 2), (3, 700, 384, 6), (1, 1024, 256, 8),
+                                   (1, 2000, 64, 2)],
+                         ids=lambda s: "B%dT%dC%dNH%d" % s)
+def test_long_blocks_split(gpu, shape):
+    """T long enough that the default backward splits its longest dK/dV and
+    dQ blocks in two halves accumulated into zeroed rows (ragged T, every
+    head size)."""
+    _case(*shape, 4321, 8765)
+
+
 def test_reference_default_shape(gpu):
     """test_flash.cu default: B=16 T=256 C=384 NH=6, seeds 1234 / 99."""
     _case(16, 256, 384, 6, 1234, 99)
