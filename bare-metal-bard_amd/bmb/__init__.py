@@ -1,9 +1,10 @@
 """ctypes binding of the gfx950 HIP library (lib/libbmb.so).
 
 This is the only way Python reaches the kernels: every call goes through the
-C-ABI entry points declared in include/kernels.h, include/gemm.h and
-include/flash.h. Pointers are raw device addresses (ints); the caller owns the
-memory (tests and bench.py use torch tensors purely as device allocations).
+C-ABI entry points declared in include/kernels.h, gemm.h, flash.h,
+attention.h, nn.h and gpt.h. Pointers are raw device addresses (ints); the
+caller owns the memory (tests and bench.py use torch tensors purely as device
+allocations), except for the GPT struct, whose buffers gpt_alloc makes.
 
 There is no fallback: if the library is missing, lib() raises.
 """
@@ -30,6 +31,48 @@ class KernelEntry(ctypes.Structure):
     _fields_ = [("id", c_int), ("name", c_char_p), ("fn", c_vp),
                 ("note", c_char_p), ("tol", c_double)]
 
+
+PARAM_NAMES = ("wte", "wpe", "ln1w", "ln1b", "qkvw", "qkvb", "attprojw", "attprojb",
+               "ln2w", "ln2b", "fcw", "fcb", "fcprojw", "fcprojb", "lnfw", "lnfb")
+ACT_NAMES = ("encoded", "ln1", "ln1_mean", "ln1_rstd", "qkv", "qkvr", "att", "atty",
+             "attproj", "lse", "residual2", "ln2", "ln2_mean", "ln2_rstd", "fch", "fch_gelu",
+             "fcproj", "residual3", "lnf", "lnf_mean", "lnf_rstd", "logits", "probs", "losses")
+GRAD_ACT_NAMES = ("dres", "dln1", "dln2", "datty", "dqkv", "dqkvr", "datt", "dsum", "dfch",
+                  "dfch_gelu", "dlogits", "dlnf")
+c_size_t = ctypes.c_size_t
+
+
+class GPTConfig(ctypes.Structure):
+    """Mirror of `struct GPTConfig` (include/gpt.h)."""
+    _fields_ = [(n, c_int) for n in ("max_seq_len", "vocab_size", "padded_vocab", "n_layer",
+                                     "n_head", "n_embd")]
+
+
+class Parameters(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in PARAM_NAMES]
+
+
+class Activations(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ACT_NAMES]
+
+
+class Gradients(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in GRAD_ACT_NAMES]
+
+
+class GPT(ctypes.Structure):
+    """Mirror of `struct GPT` (include/gpt.h)."""
+    _fields_ = [("config", GPTConfig), ("use_flash", c_bool), ("B", c_int), ("T", c_int),
+                ("params", Parameters), ("grads", Parameters),
+                ("psize", c_size_t * 16), ("num_params", c_size_t),
+                ("params_mem", c_vp), ("grads_mem", c_vp), ("m_mem", c_vp), ("v_mem", c_vp),
+                ("acts", Activations), ("gr", Gradients),
+                ("acts_mem", c_vp), ("grads_act_mem", c_vp),
+                ("num_acts", c_size_t), ("num_grad_acts", c_size_t),
+                ("d_tokens", c_vp), ("d_targets", c_vp)]
+
+
+_GPTP = ctypes.POINTER(GPT)
 
 # Every symbol the C headers declare, with its ctypes signature.
 _SIGS = {
@@ -65,9 +108,43 @@ _SIGS = {
     "flash_default_bwd_config": (c_int, []),
     "flash_attention_backward_cfg": (c_bool, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp,
                                               c_vp, c_int, c_int, c_int, c_int]),
+    # attention.h
+    "attention_forward": (None, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int]),
+    "attention_backward": (None, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
+                                  c_int, c_int]),
+    # nn.h
+    "encoder_forward": (None, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int]),
+    "encoder_backward": (None, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int]),
+    "layernorm_forward": (None, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int]),
+    "layernorm_backward": (None, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
+                                  c_int]),
+    "gelu_forward": (None, [c_vp, c_vp, c_int]),
+    "gelu_backward": (None, [c_vp, c_vp, c_vp, c_int]),
+    "residual_forward": (None, [c_vp, c_vp, c_vp, c_int]),
+    "add_inplace": (None, [c_vp, c_vp, c_int]),
+    "bias_forward": (None, [c_vp, c_vp, c_int, c_int]),
+    "bias_backward": (None, [c_vp, c_vp, c_int, c_int]),
+    "softmax_crossentropy_forward": (None, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int]),
+    "crossentropy_softmax_backward": (None, [c_vp, c_vp, c_vp, c_int, c_int, c_int,
+                                             c_float]),
+    "adamw_update": (None, [c_vp, c_vp, c_vp, c_vp, c_int, c_float, c_float, c_float,
+                            c_float, c_float, c_int, c_float]),
+    "grad_global_norm": (c_float, [c_vp, c_int]),
+    "zero_buffer": (None, [c_vp, c_size_t]),
+    "reduce_mean": (c_float, [c_vp, c_int]),
+    # gpt.h
+    "param_sizes": (None, [ctypes.POINTER(c_size_t), ctypes.POINTER(GPTConfig)]),
+    "gpt_alloc": (None, [_GPTP]),
+    "gpt_init": (None, [_GPTP, ctypes.c_uint]),
+    "gpt_forward": (c_float, [_GPTP, c_vp, c_vp]),
+    "gpt_backward": (None, [_GPTP]),
+    "gpt_free": (None, [_GPTP]),
+    "gpt_save_checkpoint": (c_int, [_GPTP, c_char_p, c_char_p, c_int]),
+    "gpt_load_checkpoint": (c_int, [_GPTP, c_char_p, c_char_p, c_int,
+                                    ctypes.POINTER(c_int)]),
 }
-# Data symbols (kernels.h).
-DATA_SYMBOLS = ("KERNELS", "NUM_KERNELS")
+# Data symbols (kernels.h, gpt.h).
+DATA_SYMBOLS = ("KERNELS", "NUM_KERNELS", "PARAM_NAMES")
 
 
 def build(jobs: int = 8) -> str:
@@ -179,3 +256,67 @@ def flash_default_config() -> int:
 
 def flash_default_bwd_config() -> int:
     return int(lib().flash_default_bwd_config())
+
+
+# ------------------------------------------------------------ attention.h / nn.h
+def call(name, *args):
+    """Calls the C entry point `name` with raw arguments (device pointers as
+    ints); returns its result."""
+    return getattr(lib(), name)(*args)
+
+
+def param_names():
+    """PARAM_NAMES as exported by the library (include/gpt.h)."""
+    arr = (c_char_p * 16).in_dll(lib(), "PARAM_NAMES")
+    return [x.decode() for x in arr]
+
+
+def param_sizes(cfg):
+    s = (c_size_t * 16)()
+    c = GPTConfig(*cfg)
+    lib().param_sizes(s, ctypes.byref(c))
+    return [int(x) for x in s]
+
+
+class Model:
+    """Owns one `struct GPT` (include/gpt.h) and forwards to the C entry points.
+
+    cfg = (max_seq_len, vocab_size, padded_vocab, n_layer, n_head, n_embd).
+    tokens/targets are host int32 arrays of B*T ids, as gpt_forward takes them.
+    """
+
+    def __init__(self, cfg, B, T, use_flash=True):
+        self.g = GPT()
+        self.g.config = GPTConfig(*cfg)
+        self.g.use_flash = bool(use_flash)
+        self.g.B, self.g.T = B, T
+        lib().gpt_alloc(ctypes.byref(self.g))
+        self._alive = True
+
+    def init(self, seed):
+        lib().gpt_init(ctypes.byref(self.g), seed)
+
+    def forward(self, tokens, targets=None):
+        import numpy as np
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        assert tok.size == self.g.B * self.g.T
+        tgt = None
+        if targets is not None:
+            tgt = np.ascontiguousarray(targets, dtype=np.int32).reshape(-1)
+            assert tgt.size == tok.size
+        return float(lib().gpt_forward(ctypes.byref(self.g), tok.ctypes.data,
+                                       tgt.ctypes.data if tgt is not None else None))
+
+    def backward(self):
+        lib().gpt_backward(ctypes.byref(self.g))
+
+    def free(self):
+        if self._alive:
+            lib().gpt_free(ctypes.byref(self.g))
+            self._alive = False
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -45,12 +45,12 @@
 #include <stdlib.h>
 
 #include <algorithm>
-#include <mutex>
 #include <vector>
 
 #include "common.hpp"
 #include "../../include/flash.h"
 #include "launch.hpp"
+#include "workspace.hpp"
 
 namespace {
 
@@ -952,28 +952,7 @@ constexpr int BWD_DEFAULT = 5;
 // streams of one device race on it (the reference's backward runs on the
 // null stream, where launches are serialised).
 float *ds_workspace(size_t bytes) {
-    static std::mutex mu;
-    static float *ptr[64] = {nullptr};
-    static size_t cap[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] < bytes) {
-        if (ptr[dev] != nullptr) {
-            if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-            (void)hipFree(ptr[dev]);
-            ptr[dev] = nullptr;
-            cap[dev] = 0;
-        }
-        void *p = nullptr;
-        if (hipMalloc(&p, bytes) != hipSuccess) {
-            (void)hipGetLastError();  // clear the allocation failure
-            return nullptr;
-        }
-        ptr[dev] = static_cast<float *>(p);
-        cap[dev] = bytes;
-    }
-    return ptr[dev];
+    return static_cast<float *>(bmb::device_scratch(bmb::SCRATCH_FLASH_DS, bytes));
 }
 
 int grid_blocks(int BH, int T, int rows_per_block) {

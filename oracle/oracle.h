@@ -1,6 +1,7 @@
 /*
- * CPU oracle for the SGEMM ladder, the transpose-aware / batched GEMM and the
- * fused causal attention of bare-metal-bard.
+ * CPU oracle for the SGEMM ladder, the transpose-aware / batched GEMM, the
+ * fused causal attention, and the transformer building blocks and GPT model
+ * built on them, of bare-metal-bard.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links or calls this
  * code; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
@@ -104,6 +105,59 @@ void orc_attn_bwd_f64(const float *qkv, const float *dout, int B, int T, int C,
  * Writes out (B,T,C) and dqkv (B,T,3C). */
 void orc_attn_fwdbwd_f32(const float *qkv, const float *dout, int B, int T,
                          int C, int NH, float *out, float *dqkv, int threads);
+
+/* ---- transformer building blocks (oracle_gpt.c) ---------------------------
+ * fp64 in, fp64 out; the fp32 values the GPU sees are widened exactly.
+ * Gradient outputs marked "+=" accumulate, as the reference's do. */
+/* out[b,t,:] = wte[tokens[b,t],:] + wpe[t,:]  (src/nn.cu:22-35) */
+void orc_encoder_fwd(double *out, const int *tokens, const double *wte,
+                     const double *wpe, int B, int T, int C);
+/* dwte[tok,:] += dout[b,t,:], dwpe[t,:] += dout[b,t,:]  (src/nn.cu:37-46) */
+void orc_encoder_bwd(double *dwte, double *dwpe, const double *dout,
+                     const int *tokens, int B, int T, int C);
+/* biased variance, eps 1e-5, rstd = 1/sqrt(var + eps)  (src/nn.cu:55-82) */
+void orc_layernorm_fwd(double *out, double *mean, double *rstd,
+                       const double *inp, const double *w, const double *b,
+                       int N, int C);
+/* dinp += rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)), dw += dy xhat,
+ * db += dy  (src/nn.cu:90-111) */
+void orc_layernorm_bwd(double *dinp, double *dw, double *db,
+                       const double *dout, const double *inp, const double *w,
+                       const double *mean, const double *rstd, int N, int C);
+/* GPT-2 tanh GELU and its derivative (src/nn.cu:116-142); dinp written */
+void orc_gelu_fwd(double *out, const double *inp, size_t n);
+void orc_gelu_bwd(double *dinp, const double *inp, const double *dout, size_t n);
+/* dbias[c] += sum_r dout[r,c]  (src/nn.cu:168-175) */
+void orc_bias_bwd(double *dbias, const double *dout, int N, int C);
+/* softmax over the first V of Vp columns, probs[V:Vp] = 0, loss =
+ * -ln(max(p[target], 1e-30)) (src/nn.cu:177-203); a target outside [0,Vp)
+ * gives NaN. losses may be NULL. */
+void orc_softmax_xent_fwd(double *probs, double *losses, const double *logits,
+                          const int *targets, int N, int V, int Vp);
+/* dlogits = (p - [i == target]) * scale for i < V, 0 beyond
+ * (src/nn.cu:208-219) */
+void orc_xent_bwd(double *dlogits, const double *probs, const int *targets,
+                  int N, int V, int Vp, double scale);
+/* fp32 AdamW restated operation by operation (src/nn.cu:300-319, bias
+ * corrections 1 - powf(beta, step) as at src/nn.cu:326-329). */
+void orc_adamw_f32(float *params, const float *grads, float *m, float *v,
+                   size_t n, float lr, float beta1, float beta2, float eps,
+                   float wd, int step, float grad_scale);
+
+/* ---- GPT model (oracle_gpt.c) ----------------------------------------------
+ * cfg = {max_seq_len, vocab_size, padded_vocab, n_layer, n_head, n_embd}, the
+ * field order of GPTConfig (src/gpt.h:10-17). */
+/* The 16 parameter tensor sizes in PARAM_NAMES order (src/gpt.cu:32-50). */
+void orc_gpt_param_sizes(size_t *s, const int cfg[6]);
+/* Forward of src/gpt.cu:228-300 and, when grads != NULL, the backward of
+ * src/gpt.cu:303-386 (grads written, fp64, flat in parameter order), with
+ * the unfused attention of src/attention.cu as the attention. params is the
+ * flat parameter vector in fp64. Returns the mean loss; losses_out (N) and
+ * logits_out (N x Vp) are filled when not NULL. */
+double orc_gpt_forward_backward(const int cfg[6], int B, int T,
+                                const double *params, const int *tokens,
+                                const int *targets, double *losses_out,
+                                double *grads, double *logits_out);
 
 /* Number of threads OpenMP would use by default (for reporting). */
 int orc_max_threads(void);

@@ -20,6 +20,8 @@ _lib = None
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_szp = np.ctypeslib.ndpointer(dtype=np.uintp, flags="C_CONTIGUOUS")
 
 
 def build() -> str:
@@ -56,6 +58,22 @@ def lib():
     L.orc_dsum_f64.argtypes = [_f32p, _f32p, i, i, i, i, _f64p]
     L.orc_attn_bwd_f64.argtypes = [_f32p, _f32p, i, i, i, i, _f64p]
     L.orc_attn_fwdbwd_f32.argtypes = [_f32p, _f32p, i, i, i, i, _f32p, _f32p, i]
+    L.orc_encoder_fwd.argtypes = [_f64p, _i32p, _f64p, _f64p, i, i, i]
+    L.orc_encoder_bwd.argtypes = [_f64p, _f64p, _f64p, _i32p, i, i, i]
+    L.orc_layernorm_fwd.argtypes = [_f64p, _f64p, _f64p, _f64p, _f64p, _f64p, i, i]
+    L.orc_layernorm_bwd.argtypes = [_f64p, _f64p, _f64p, _f64p, _f64p, _f64p, _f64p,
+                                    _f64p, i, i]
+    L.orc_gelu_fwd.argtypes = [_f64p, _f64p, sz]
+    L.orc_gelu_bwd.argtypes = [_f64p, _f64p, _f64p, sz]
+    L.orc_bias_bwd.argtypes = [_f64p, _f64p, i, i]
+    L.orc_softmax_xent_fwd.argtypes = [_f64p, _f64p, _f64p, _i32p, i, i, i]
+    L.orc_xent_bwd.argtypes = [_f64p, _f64p, _i32p, i, i, i, d]
+    L.orc_adamw_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, f, f, f, f, f, i, f]
+    L.orc_gpt_param_sizes.argtypes = [_szp, _i32p]
+    L.orc_gpt_forward_backward.argtypes = [_i32p, i, i, _f64p, _i32p, _i32p,
+                                           ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_void_p]
+    L.orc_gpt_forward_backward.restype = d
     L.orc_max_threads.restype = i
     _lib = L
     return L
@@ -169,3 +187,111 @@ def attn_fwdbwd_f32(qkv, dout, B, T, C, NH, threads: int = 0):
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ---------------------------------------------------------------- nn ops
+def _d(a):
+    return np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+
+
+def _i(a):
+    return np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
+
+
+def encoder_fwd(tokens, wte, wpe, B, T, C):
+    out = np.empty(B * T * C, np.float64)
+    lib().orc_encoder_fwd(out, _i(tokens), _d(wte), _d(wpe), B, T, C)
+    return out.reshape(B * T, C)
+
+
+def encoder_bwd(dwte0, dwpe0, dout, tokens, B, T, C):
+    dwte, dwpe = _d(dwte0).copy(), _d(dwpe0).copy()
+    lib().orc_encoder_bwd(dwte, dwpe, _d(dout), _i(tokens), B, T, C)
+    return dwte, dwpe
+
+
+def layernorm_fwd(inp, w, b, N, C):
+    out = np.empty(N * C, np.float64)
+    mean = np.empty(N, np.float64)
+    rstd = np.empty(N, np.float64)
+    lib().orc_layernorm_fwd(out, mean, rstd, _d(inp), _d(w), _d(b), N, C)
+    return out.reshape(N, C), mean, rstd
+
+
+def layernorm_bwd(dinp0, dw0, db0, dout, inp, w, mean, rstd, N, C):
+    dinp, dw, db = _d(dinp0).copy(), _d(dw0).copy(), _d(db0).copy()
+    lib().orc_layernorm_bwd(dinp, dw, db, _d(dout), _d(inp), _d(w), _d(mean), _d(rstd),
+                            N, C)
+    return dinp.reshape(N, C), dw, db
+
+
+def gelu_fwd(x):
+    x = _d(x)
+    out = np.empty_like(x)
+    lib().orc_gelu_fwd(out, x, x.size)
+    return out
+
+
+def gelu_bwd(x, dout):
+    x = _d(x)
+    out = np.empty_like(x)
+    lib().orc_gelu_bwd(out, x, _d(dout), x.size)
+    return out
+
+
+def bias_bwd(dbias0, dout, N, C):
+    db = _d(dbias0).copy()
+    lib().orc_bias_bwd(db, _d(dout), N, C)
+    return db
+
+
+def softmax_xent_fwd(logits, targets, N, V, Vp):
+    probs = np.empty(N * Vp, np.float64)
+    losses = np.empty(N, np.float64)
+    lib().orc_softmax_xent_fwd(probs, losses, _d(logits), _i(targets), N, V, Vp)
+    return probs.reshape(N, Vp), losses
+
+
+def xent_bwd(probs, targets, N, V, Vp, scale):
+    out = np.empty(N * Vp, np.float64)
+    lib().orc_xent_bwd(out, _d(probs), _i(targets), N, V, Vp, float(scale))
+    return out.reshape(N, Vp)
+
+
+def adamw_f32(params, grads, m, v, lr, beta1, beta2, eps, wd, step, grad_scale):
+    """Returns updated copies (params, m, v)."""
+    p = _c(params).reshape(-1).copy()
+    mm = _c(m).reshape(-1).copy()
+    vv = _c(v).reshape(-1).copy()
+    lib().orc_adamw_f32(p, _c(grads).reshape(-1), mm, vv, p.size, lr, beta1, beta2, eps,
+                        wd, int(step), grad_scale)
+    return p, mm, vv
+
+
+# ---------------------------------------------------------------- GPT
+PARAM_NAMES = ("wte", "wpe", "ln1w", "ln1b", "qkvw", "qkvb", "attprojw", "attprojb",
+               "ln2w", "ln2b", "fcw", "fcb", "fcprojw", "fcprojb", "lnfw", "lnfb")
+
+
+def gpt_param_sizes(cfg):
+    """cfg = (max_seq_len, vocab_size, padded_vocab, n_layer, n_head, n_embd)."""
+    s = np.zeros(16, np.uintp)
+    lib().orc_gpt_param_sizes(s, _i(cfg))
+    return [int(x) for x in s]
+
+
+def gpt_forward_backward(cfg, B, T, params, tokens, targets, grads=True, logits=False):
+    """fp64 GPT forward (+ backward). Returns (mean_loss, losses, grads|None,
+    logits|None); params is the flat parameter vector (widened to fp64)."""
+    p = _d(params)
+    n = sum(gpt_param_sizes(cfg))
+    assert p.size == n, (p.size, n)
+    N = B * T
+    losses = np.empty(N, np.float64)
+    g = np.empty(n, np.float64) if grads else None
+    lg = np.empty(N * cfg[2], np.float64) if logits else None
+    loss = lib().orc_gpt_forward_backward(
+        _i(cfg), B, T, p, _i(tokens), _i(targets), losses.ctypes.data,
+        g.ctypes.data if g is not None else None,
+        lg.ctypes.data if lg is not None else None)
+    return float(loss), losses, g, (lg.reshape(N, cfg[2]) if lg is not None else None)

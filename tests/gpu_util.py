@@ -65,3 +65,37 @@ class Guarded:
         h = host(self.buf.view(torch.int32))
         c = np.int32(np.uint32(CANARY).view(np.int32))
         return bool((h[:GUARD] == c).all() and (h[GUARD + self.n:] == c).all())
+
+
+# ---- raw device pointers owned by the library (the GPT struct's buffers)
+_hip = None
+
+
+def _hiprt():
+    """The HIP runtime already loaded in this process (torch and libbmb share
+    one libamdhip64.so.7)."""
+    global _hip
+    if _hip is None:
+        import ctypes
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                   ctypes.c_int]
+        _hip.hipMemcpy.restype = ctypes.c_int
+    return _hip
+
+
+def d2h(ptr, n, dtype=np.float32):
+    """Copies n elements at device address ptr into a new host array."""
+    out = np.empty(n, dtype)
+    if n:
+        e = _hiprt().hipMemcpy(out.ctypes.data, ptr, out.nbytes, 2)
+        assert e == 0, "hipMemcpy D2H failed: %d" % e
+    return out
+
+
+def h2d(ptr, a):
+    """Copies host array a to device address ptr."""
+    a = np.ascontiguousarray(a)
+    if a.size:
+        e = _hiprt().hipMemcpy(ptr, a.ctypes.data, a.nbytes, 1)
+        assert e == 0, "hipMemcpy H2D failed: %d" % e

@@ -10,7 +10,8 @@ import pytest
 import bmb
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("kernels.h", "gemm.h", "flash.h")]
+HEADERS = [os.path.join(ROOT, "include", h)
+           for h in ("kernels.h", "gemm.h", "flash.h", "attention.h", "nn.h", "gpt.h")]
 
 
 def _declared():
@@ -23,7 +24,11 @@ def _declared():
             if name in ("if", "sizeof", "defined", "sgemm_fn", "void") or name.startswith("BMB_"):
                 continue
             names.add(name)
+        # the C++ view's inline overloads are not exported symbols
+        names.discard("return")
         for m in re.finditer(r"extern\s+const\s+\w+\s+(\w+)", src):
+            names.add(m.group(1))
+        for m in re.finditer(r"extern\s+const\s+char\s*\*\s*const\s+(\w+)", src):
             names.add(m.group(1))
     return names
 
@@ -90,3 +95,37 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(bmb, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError):
         bmb.lib()
+
+
+def test_gpt_struct_layout_matches_header(tmp_path):
+    """The ctypes mirror of struct GPT has the C header's size and offsets
+    (compiled with the host C compiler; no GPU)."""
+    import subprocess
+    fields = [f[0] for f in bmb.GPT._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "gpt.h"', "int main(void){",
+           'printf("%zu\\n", sizeof(GPT));']
+    src += ['printf("%%zu\\n", offsetof(GPT, %s));' % f for f in fields]
+    src += ['printf("%%zu\\n", offsetof(Activations, %s));' % f for f in bmb.ACT_NAMES]
+    src += ['printf("%%zu\\n", offsetof(Gradients, %s));' % f for f in bmb.GRAD_ACT_NAMES]
+    src += ["return 0;}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(c), "-o",
+                    str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    want = [ctypes.sizeof(bmb.GPT)] + [getattr(bmb.GPT, f).offset for f in fields]
+    want += [getattr(bmb.Activations, f).offset for f in bmb.ACT_NAMES]
+    want += [getattr(bmb.Gradients, f).offset for f in bmb.GRAD_ACT_NAMES]
+    assert got == want
+
+
+def test_gpt_param_sizes_and_names():
+    """param_sizes is host code: compare with the oracle's src/gpt.cu:32-50
+    restatement at the GPT-2 small config and the gradient-check config."""
+    import oracle as O
+    for cfg in ((1024, 50257, 50304, 12, 12, 768), (64, 65, 128, 2, 4, 128)):
+        assert bmb.param_sizes(cfg) == O.gpt_param_sizes(cfg)
+    assert sum(bmb.param_sizes((1024, 50257, 50304, 12, 12, 768))) == 124475904
+    assert bmb.param_names() == list(bmb.PARAM_NAMES) == list(O.PARAM_NAMES)

@@ -1,0 +1,260 @@
+"""The GPT model (gpt.h) on the GPU against the fp64 CPU oracle.
+
+Config of tools/test_grad.cu:57 -- B=4, T=64, C=128, L=2, NH=4, V=65 (Vp=128)
+-- with both attention paths (fused flash and the unfused attention.h):
+  * forward loss, per-position losses and logits against the oracle's fp64
+    GPT (oracle/oracle_gpt.c, itself pinned to torch autograd), and every
+    parameter gradient, tensor by tensor;
+  * tools/test_grad.cu's directional-derivative check run on the GPU model
+    itself (eps 1e-2, relative error < 2e-2 per tensor and for ALL);
+  * a short AdamW training run (global-norm clipping at 1.0) whose loss
+    trajectory follows the oracle's (fp64 model, fp32 AdamW restatement);
+  * invariants: wte = 0 gives loss = ln V exactly; repeated steps are
+    bit-identical; gpt_init statistics; the GPT1 checkpoint round trip.
+Tolerances: fp32 arithmetic through two layers against fp64 -- loss 1e-5
+relative, logits and each gradient tensor 1e-4 normwise (the measured errors
+are printed; they sit near 1e-6).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import bmb
+import oracle as O
+from gpu_util import d2h, h2d, sync
+
+pytestmark = pytest.mark.gpu
+
+CFG = (64, 65, 128, 2, 4, 128)  # max_seq_len, V, Vp, L, NH, C
+B, T = 4, 64
+
+
+def _batch(seed, V=CFG[1], n=B * T):
+    r = np.random.default_rng(seed)
+    return r.integers(0, V, n).astype(np.int32), r.integers(0, V, n).astype(np.int32)
+
+
+def _model(use_flash, seed=1337, cfg=CFG, b=B, t=T):
+    m = bmb.Model(cfg, b, t, use_flash=use_flash)
+    m.init(seed)
+    sync("gpt_init")
+    return m
+
+
+def _params(m):
+    return d2h(m.g.params_mem, m.g.num_params)
+
+
+def _grads(m):
+    return d2h(m.g.grads_mem, m.g.num_params)
+
+
+def _offsets(cfg=CFG):
+    return np.cumsum([0] + O.gpt_param_sizes(cfg))
+
+
+@pytest.mark.parametrize("use_flash", [True, False], ids=["flash", "unfused"])
+def test_forward_backward_vs_oracle(gpu, use_flash):
+    m = _model(use_flash)
+    x, y = _batch(4242)
+    print("gpt fwd/bwd use_flash=%s" % use_flash, flush=True)
+    loss = m.forward(x, y)
+    m.backward()
+    sync("gpt forward/backward")
+    p = _params(m)
+    ref_loss, ref_losses, ref_g, ref_logits = O.gpt_forward_backward(CFG, B, T, p, x, y,
+                                                                     logits=True)
+    losses = d2h(m.g.acts.losses, B * T)
+    logits = d2h(m.g.acts.logits, B * T * CFG[2]).reshape(B * T, CFG[2])
+    print("loss gpu %.8f oracle %.8f" % (loss, ref_loss))
+    assert abs(loss - ref_loss) <= 1e-5 * ref_loss
+    assert np.abs(losses - ref_losses).max() <= 1e-5 * ref_loss
+    el = O.normwise(logits, ref_logits)[0]
+    assert el < 1e-4, el
+    g = _grads(m)
+    off = _offsets()
+    worst = 0.0
+    for t, name in enumerate(O.PARAM_NAMES):
+        e, bad = O.normwise(g[off[t]:off[t + 1]], ref_g[off[t]:off[t + 1]])
+        print("  %-9s normwise %.2e" % (name, e))
+        assert bad == 0 and e < 1e-4, name
+        worst = max(worst, e)
+    print("logits %.2e, worst gradient %.2e" % (el, worst))
+
+
+def _loss_double(m, x, y):
+    """Mean loss with the per-position losses summed in fp64 on the host
+    (tools/test_grad.cu:44-52)."""
+    m.forward(x, y)
+    return float(d2h(m.g.acts.losses, B * T).astype(np.float64).mean())
+
+
+@pytest.mark.parametrize("use_flash", [True, False], ids=["flash", "unfused"])
+def test_directional_derivative_gradcheck(gpu, use_flash):
+    """tools/test_grad.cu:77-176 on the GPU model: for each tensor step along
+    u = g/||g||; (L(p + eps u) - L(p - eps u)) / 2 eps must match ||g||."""
+    eps = 1e-2
+    m = _model(use_flash)
+    x, y = _batch(4242)
+    L0 = _loss_double(m, x, y)
+    m.backward()
+    g = _grads(m).astype(np.float64)
+    p = _params(m)
+    off = _offsets()
+    print("loss at theta %.6f (ln V = %.6f)" % (L0, math.log(CFG[1])))
+    failures, checked = [], 0
+    dirs = [(name, off[t], off[t + 1]) for t, name in enumerate(O.PARAM_NAMES)]
+    dirs.append(("ALL", 0, p.size))
+    for name, a, b in dirs:
+        gt = g[a:b]
+        gn = float(np.sqrt((gt * gt).sum()))
+        if gn < 1e-9:
+            print("  %-9s skipped (zero grad)" % name)
+            continue
+        pp = p.copy()
+        pp[a:b] = (p[a:b] + eps * (gt / gn)).astype(np.float32)
+        h2d(m.g.params_mem, pp)
+        lp = _loss_double(m, x, y)
+        pp[a:b] = (p[a:b] - eps * (gt / gn)).astype(np.float32)
+        h2d(m.g.params_mem, pp)
+        lm = _loss_double(m, x, y)
+        num = (lp - lm) / (2 * eps)
+        rel = abs(num - gn) / max(gn, 1e-12)
+        print("  %-9s analytic %.6e numeric %.6e rel %.2e" % (name, gn, num, rel))
+        checked += 1
+        if not rel < 2e-2:
+            failures.append(name)
+        h2d(m.g.params_mem, p)
+    assert checked >= 15 and not failures, failures
+
+
+def test_steps_are_deterministic(gpu):
+    m = _model(True)
+    x, y = _batch(7)
+    l1 = m.forward(x, y)
+    m.backward()
+    g1 = _grads(m)
+    l2 = m.forward(x, y)
+    m.backward()
+    g2 = _grads(m)
+    assert l1 == l2 and np.array_equal(g1, g2)
+
+
+def test_zero_embedding_gives_ln_v(gpu):
+    """wte = 0 makes every logit 0: loss = ln V for every position."""
+    m = _model(True)
+    h2d(m.g.params_mem, np.zeros(m.g.psize[0], np.float32))
+    x, y = _batch(9)
+    loss = m.forward(x, y)
+    losses = d2h(m.g.acts.losses, B * T)
+    assert abs(loss - math.log(CFG[1])) < 1e-6
+    assert np.abs(losses - math.log(CFG[1])).max() < 1e-6
+    assert not np.any(d2h(m.g.acts.logits, B * T * CFG[2]))
+
+
+def _train(use_gpu_model, steps, lr=1e-3, wd=0.1, clip=1.0):
+    """Losses of `steps` AdamW steps on one fixed batch: the GPU model, or
+    the oracle's fp64 model with the fp32 AdamW restatement."""
+    m = _model(True)
+    x, y = _batch(11)
+    losses = []
+    if use_gpu_model:
+        for step in range(1, steps + 1):
+            losses.append(m.forward(x, y))
+            m.backward()
+            gn = bmb.call("grad_global_norm", m.g.grads_mem, m.g.num_params)
+            gs = clip / gn if gn > clip else 1.0
+            bmb.call("adamw_update", m.g.params_mem, m.g.grads_mem, m.g.m_mem, m.g.v_mem,
+                     m.g.num_params, lr, 0.9, 0.999, 1e-8, wd, step, gs)
+        sync("train")
+        return losses
+    p = _params(m)
+    mm = np.zeros_like(p)
+    vv = np.zeros_like(p)
+    for step in range(1, steps + 1):
+        loss, _, g, _ = O.gpt_forward_backward(CFG, B, T, p, x, y)
+        losses.append(loss)
+        g32 = g.astype(np.float32)
+        gn = float(np.sqrt((g32.astype(np.float64) ** 2).sum()))
+        gs = clip / gn if gn > clip else 1.0
+        p, mm, vv = O.adamw_f32(p, g32, mm, vv, lr, 0.9, 0.999, 1e-8, wd, step, gs)
+    return losses
+
+
+def test_training_trajectory_tracks_oracle(gpu):
+    steps = 8
+    gpu_l = _train(True, steps)
+    ref_l = _train(False, steps)
+    print("gpu   ", " ".join("%.6f" % v for v in gpu_l))
+    print("oracle", " ".join("%.6f" % v for v in ref_l))
+    assert gpu_l[-1] < gpu_l[0] - 0.05  # it learns the batch
+    for a, b in zip(gpu_l, ref_l):
+        assert abs(a - b) <= 2e-4 * b, (a, b)
+
+
+def test_init_statistics_and_seed(gpu):
+    cfg = (64, 65, 128, 4, 4, 128)
+    m = _model(True, seed=1337, cfg=cfg)
+    p = _params(m)
+    off = _offsets(cfg)
+    sl = {n: p[off[t]:off[t + 1]] for t, n in enumerate(O.PARAM_NAMES)}
+    for n in ("ln1w", "ln2w", "lnfw"):
+        assert np.all(sl[n] == 1.0)
+    for n in ("ln1b", "ln2b", "lnfb", "qkvb", "attprojb", "fcb", "fcprojb"):
+        assert not np.any(sl[n])
+    for n in ("wte", "wpe", "qkvw", "fcw"):
+        assert abs(sl[n].std() / 0.02 - 1) < 0.02 and abs(sl[n].mean()) < 1e-3, n
+    rs = 0.02 / math.sqrt(2 * cfg[3])
+    for n in ("attprojw", "fcprojw"):
+        assert abs(sl[n].std() / rs - 1) < 0.02, n
+    m2 = _model(True, seed=1337, cfg=cfg)
+    assert np.array_equal(_params(m2), p)
+    m3 = _model(True, seed=1338, cfg=cfg)
+    assert not np.array_equal(_params(m3), p)
+
+
+def test_checkpoint_roundtrip(gpu, tmp_path):
+    import ctypes
+    m = _model(True)
+    path = str(tmp_path / "gpt.bin").encode()
+    itos = bytes(range(32, 32 + CFG[1]))
+    assert bmb.call("gpt_save_checkpoint", ctypes.byref(m.g), path, itos, len(itos)) == 0
+    raw = np.fromfile(tmp_path / "gpt.bin", dtype=np.uint8)
+    assert raw[:4].view(np.int32)[0] == 0x47505431
+    assert list(raw[4:28].view(np.int32)) == list(CFG)
+    g2 = bmb.GPT()
+    g2.B, g2.use_flash = B, True
+    buf = ctypes.create_string_buffer(256)
+    nv = ctypes.c_int(0)
+    assert bmb.call("gpt_load_checkpoint", ctypes.byref(g2), path, buf, 256, ctypes.byref(nv)) == 0
+    assert nv.value == len(itos) and buf.raw[:len(itos)] == itos
+    assert g2.T == CFG[0] and tuple(getattr(g2.config, f) for f, _ in bmb.GPTConfig._fields_) == CFG
+    assert np.array_equal(d2h(g2.params_mem, g2.num_params), _params(m))
+    bmb.call("gpt_free", ctypes.byref(g2))
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(b"XXXX" + bytes(64))
+    g3 = bmb.GPT()
+    g3.B = B
+    assert bmb.call("gpt_load_checkpoint", ctypes.byref(g3), str(bad).encode(), None, 0, None) == -1
+
+
+def test_gpt2_small_first_step(gpu):
+    """GPT-2 small (12L/768/12H, T=1024, V=50257 -> 50304), B=2: the first
+    loss sits near ln V (logits start small), the gradients are finite and
+    the step is deterministic."""
+    cfg = (1024, 50257, 50304, 12, 12, 768)
+    m = _model(True, cfg=cfg, b=2, t=1024)
+    r = np.random.default_rng(5)
+    x = r.integers(0, cfg[1], 2 * 1024).astype(np.int32)
+    y = r.integers(0, cfg[1], 2 * 1024).astype(np.int32)
+    l1 = m.forward(x, y)
+    m.backward()
+    gn1 = bmb.call("grad_global_norm", m.g.grads_mem, m.g.num_params)
+    l2 = m.forward(x, y)
+    m.backward()
+    gn2 = bmb.call("grad_global_norm", m.g.grads_mem, m.g.num_params)
+    print("GPT-2 small loss %.5f (ln V %.5f), |g| %.5f" % (l1, math.log(cfg[1]), gn1))
+    assert abs(l1 - math.log(cfg[1])) < 0.5
+    assert np.isfinite(gn1) and gn1 > 0
+    assert l1 == l2 and gn1 == gn2
