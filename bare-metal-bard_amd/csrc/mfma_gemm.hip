@@ -5,18 +5,24 @@
 // (src/gemm.cu:204-217); batched_gemm() always uses a guarded 64x64 kernel
 // (src/bgemm.cu:88-97). Here one kernel template handles every shape and
 // transpose in-kernel (guarded, zero-filled staging; guarded stores), and the
-// host only picks the tile size (pick_tile) and whether every row of the
-// operands is 16-byte aligned.
+// host picks the tile size and a split of K (pick()) and whether every row of
+// the operands is 16-byte aligned.
+#include <math.h>
+
+#include <algorithm>
+
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
 #include "../../include/kernels.h"
 #include "launch.hpp"
+#include "workspace.hpp"
 
 namespace {
 
 using bmb::MfmaTile;
 using TileL = MfmaTile<256, 256, 16, 2, 4>;  // 512 lanes, 128x64 per wave
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
+using TileN = MfmaTile<64, 128, 16, 2, 2>;   // 256 lanes, 32x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
 
 // Number of CUs of the current device (256 on MI355X), cached per device.
@@ -34,18 +40,89 @@ int device_cus() {
     return cached[dev];
 }
 
-// Tile choice. Measured on MI355X at fp32 (N=4096/8192): the 256x256 tile
-// (8 waves, one workgroup per CU) reaches ~86% of the MFMA peak, 128x128 (4
-// waves, three per CU) ~82% and 64x64 (4 waves, eight per CU) ~78%. The big
-// tiles lose badly when their count leaves a partial round of workgroups
-// (4097^3 on 256x256: 17*17 = 289 tiles = 1.13 rounds, 63 TFLOP/s against
-// 102 on 64x64), and small problems need the small tile to occupy every CU.
-// So a big tile is used only when it fills whole rounds of the machine.
-enum class TileKind { L, M, S };
-TileKind pick_tile(long long tiles_l, long long tiles_m, int cus) {
-    if (tiles_l >= cus && tiles_l % cus == 0) return TileKind::L;
-    if (tiles_m >= 3LL * cus && tiles_m % (3LL * cus) == 0) return TileKind::M;
-    return TileKind::S;
+// Tile and split-K choice from a time model fitted to MI355X measurements of
+// every tile and split on the GPT-2 training shapes and the square sweep
+// 512 ... 8192 (both transposes). Per tile: `eff`, the fraction of the fp32
+// MFMA peak a CU reaches when it is full of such workgroups, and `occ`, the
+// workgroups that share a CU. A work item is one output tile over one K
+// split; the machine runs cus * occ of them per round, so an item count just
+// above a whole number of rounds costs a nearly empty extra round (4097^3 on
+// 256x256: 289 tiles on 256 CUs). Splitting K multiplies the items of a
+// problem with few output tiles (768 x 768 x 8192 has 144 on 64x64) and costs
+// the partials' round trip through HBM plus one reduce launch. The model only
+// compares candidates; its times are not predictions.
+enum class TileKind { L, M, N, S };
+struct Cand {
+    TileKind kind;
+    int bm, bn;
+    double eff;
+    int occ;
+};
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.894, 1},
+                          {TileKind::M, 128, 128, 0.842, 2},
+                          {TileKind::N, 64, 128, 0.730, 4},
+                          {TileKind::S, 64, 64, 0.691, 6}};
+constexpr int SPLITS[] = {1, 2, 3, 4, 6, 8};
+constexpr double K_OVERHEAD = 32.0;       // per-item prologue/epilogue, in k steps
+constexpr double HBM_BYTES_PER_S = 5e12;  // achieved, for the partials' round trip
+constexpr double LAUNCH_S = 4e-6;         // the reduce launch
+constexpr int MIN_SPLIT_K = 128;          // shortest K range a split may get
+// Largest split-K partial buffer (floats): 256 MiB per host thread and device.
+constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;
+
+struct Plan {
+    Cand tile;
+    int splits;  // number of K ranges (1: no split)
+    int kchunk;  // K per range, a multiple of 16
+};
+
+inline int round_up16(long long x) { return (int)((x + 15) / 16 * 16); }
+
+double model_time(long long M, long long N, long long K, long long batch, const Cand &c,
+                  int splits, int kchunk, int cus) {
+    const long long tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+    const long long items = tiles * splits;
+    const long long slots = (long long)cus * c.occ;
+    const double peak_cu = 157.3e12 / 256.0;
+    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) / (c.eff * peak_cu) * c.occ;
+    const long long full = items / slots, rem = items % slots;
+    double t = full * t_item;
+    if (rem) {
+        // A partial round: CUs holding fewer than occ items run each faster,
+        // but one item alone does not get the whole CU.
+        const long long per_cu = (rem + cus - 1) / cus;
+        t += per_cu < c.occ ? t_item * std::max<long long>(per_cu, std::min(c.occ, 2)) / c.occ
+                            : t_item;
+    }
+    if (splits > 1) t += (splits + 2.0) * M * N * 4.0 / HBM_BYTES_PER_S + LAUNCH_S;
+    return t;
+}
+
+// Split-K is used only for single problems on the null stream: its partials
+// live in a per-thread scratch buffer, and only the null stream orders a
+// thread's launches.
+Plan pick(int M, int N, int K, int batch, bool may_split) {
+    const int cus = device_cus();
+    Plan best{CANDS[0], 1, round_up16(K)};
+    double best_t = -1.0;
+    for (const Cand &c : CANDS) {
+        for (int s : SPLITS) {
+            int splits = 1, kchunk = round_up16(K);
+            if (s > 1) {
+                if (!may_split || K < 2 * MIN_SPLIT_K) continue;
+                kchunk = round_up16((K + s - 1) / s);
+                if (kchunk < MIN_SPLIT_K) continue;
+                splits = (K + kchunk - 1) / kchunk;
+                if (splits < 2 || (long long)splits * M * N > MAX_SPLIT_FLOATS) continue;
+            }
+            const double t = model_time(M, N, K, batch, c, splits, kchunk, cus);
+            if (best_t < 0 || t < best_t) {
+                best_t = t;
+                best = Plan{c, splits, kchunk};
+            }
+        }
+    }
+    return best;
 }
 
 template <bool TA, bool TB, class Tile>
@@ -55,16 +132,39 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, batch);
-    bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true>, L::SMEM_BYTES);
-    bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false>, L::SMEM_BYTES);
-    if (vec)
+    if (vec) {
+        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
                     sC, tiles_m, tiles_n);
-    else
+    } else {
+        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
                     sC, tiles_m, tiles_n);
+    }
+}
+
+// Split-K: the partial sums of each K range go to P (splits x M x N), then
+// one reduce kernel adds them in range order and applies alpha / beta.
+template <bool TA, bool TB, class Tile>
+void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *A,
+                  const float *B, float beta, float *C, float *P, bool vec) {
+    using L = bmb::MfmaLayout<TA, TB, Tile>;
+    const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
+    const dim3 grid(tiles_m * tiles_n, p.splits);
+    if (vec) {
+        bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, L::SMEM_BYTES);
+        bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
+                    L::SMEM_BYTES, nullptr, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+    } else {
+        bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, L::SMEM_BYTES);
+        bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
+                    L::SMEM_BYTES, nullptr, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+    }
+    const long long mn = (long long)M * N;
+    bmb::launch(bmb::splitk_reduce_k, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
+                nullptr, C, (const float *)P, p.splits, mn, alpha, beta);
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -80,15 +180,31 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const int a_contig = TA ? M : K, b_contig = TB ? K : N;
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && al16(A) && al16(B) &&
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
-    auto work = [&](int bm, int bn) {
-        return (long long)bmb::ceil_div(M, bm) * bmb::ceil_div(N, bn) * batch;
-    };
-    switch (pick_tile(work(TileL::BM, TileL::BN), work(TileM::BM, TileM::BN), device_cus())) {
+    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr);
+    float *P = nullptr;
+    if (p.splits > 1) {
+        P = static_cast<float *>(
+            bmb::device_scratch(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float)));
+        if (P == nullptr) p = pick(M, N, K, batch, false);  // no scratch: no split
+    }
+    if (p.splits > 1) {
+        switch (p.tile.kind) {
+        case TileKind::L: launch_split<TA, TB, TileL>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
+        case TileKind::M: launch_split<TA, TB, TileM>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
+        case TileKind::N: launch_split<TA, TB, TileN>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
+        case TileKind::S: launch_split<TA, TB, TileS>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
+        }
+        return;
+    }
+    switch (p.tile.kind) {
     case TileKind::L:
         launch_tile<TA, TB, TileL>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
         break;
     case TileKind::M:
         launch_tile<TA, TB, TileM>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        break;
+    case TileKind::N:
+        launch_tile<TA, TB, TileN>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
         break;
     case TileKind::S:
         launch_tile<TA, TB, TileS>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);

@@ -75,17 +75,18 @@ struct MfmaLayout {
 
 // Loads one operand chunk (4 floats along the operand's contiguous axis) from
 // global memory, zero filling whatever lies outside [0, rows) x [0, cols).
-// `row` and `col0` index the stored matrix (rows x cols, row-major).
-// VEC: cols % 4 == 0 and a 16-byte aligned base, so an in-range chunk is one
-// aligned 128-bit load. Otherwise a chunk that lies wholly inside the row is
-// still one 128-bit load (global loads on gfx950 need only dword alignment)
-// and only a chunk straddling the row end falls back to guarded 32-bit loads.
+// `row` and `col0` index the stored matrix (row stride ld floats).
+// VEC: ld % 4 == 0 and a 16-byte aligned base, so an in-range chunk is one
+// aligned 128-bit load (cols is then a multiple of 4 too). Otherwise a chunk
+// that lies wholly inside the row is still one 128-bit load (global loads on
+// gfx950 need only dword alignment) and only a chunk straddling the row end
+// falls back to guarded 32-bit loads.
 template <bool VEC>
-__device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols,
+__device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols, int ld,
                                              int row, int col0) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (row >= rows) return v;
-    const float *p = P + (size_t)row * cols + col0;
+    const float *p = P + (size_t)row * ld + col0;
     if (VEC) {
         if (col0 < cols) v = ld4(p);
     } else if (col0 + 3 < cols) {
@@ -119,23 +120,25 @@ struct MfmaGemm {
         else    { r = e / (BN / 4); c = (e % (BN / 4)) * 4; }  // stored K x N
     }
 
+    // K bounds the k index (a split's length); lda / ldb are the stored
+    // row strides (TA ? M : full K, TB ? full K : N).
     __device__ static __forceinline__ void load(Regs &g, const float *A,
                                                 const float *B, int M, int N,
-                                                int K, int m0, int n0, int k0,
-                                                int tid) {
+                                                int K, int lda, int ldb, int m0,
+                                                int n0, int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < L::A_PER_T; ++i) {
             int r, c;
             a_chunk(tid + i * NT, r, c);
-            g.a[i] = TA ? load_chunk<VEC>(A, K, M, k0 + r, m0 + c)
-                        : load_chunk<VEC>(A, M, K, m0 + r, k0 + c);
+            g.a[i] = TA ? load_chunk<VEC>(A, K, M, lda, k0 + r, m0 + c)
+                        : load_chunk<VEC>(A, M, K, lda, m0 + r, k0 + c);
         }
 #pragma unroll
         for (int i = 0; i < L::B_PER_T; ++i) {
             int r, c;
             b_chunk(tid + i * NT, r, c);
-            g.b[i] = TB ? load_chunk<VEC>(B, N, K, n0 + r, k0 + c)
-                        : load_chunk<VEC>(B, K, N, k0 + r, n0 + c);
+            g.b[i] = TB ? load_chunk<VEC>(B, N, K, ldb, n0 + r, k0 + c)
+                        : load_chunk<VEC>(B, K, N, ldb, k0 + r, n0 + c);
         }
     }
 
@@ -200,8 +203,13 @@ struct MfmaGemm {
                                                                        acc[fi][fn], 0, 0, 0);
     }
 
-    // One output tile (m0, n0) of one problem. smem holds two stages.
-    __device__ static __forceinline__ void run(int M, int N, int K, float alpha,
+    // One output tile (m0, n0) of one problem over k in [0, K); A and B are
+    // positioned at k = 0 of that range, lda / ldb are their row strides.
+    // smem holds two stages. PARTIAL: store the raw fp32 sums to C (an
+    // M x N split-K partial) instead of applying the alpha/beta epilogue.
+    template <bool PARTIAL = false>
+    __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
+                                               float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B,
                                                float beta, float *C, int m0,
@@ -223,9 +231,9 @@ struct MfmaGemm {
         const int nkt = (K + BK - 1) / BK;
         if (nkt > 0) {
             Regs g;
-            load(g, A, B, M, N, K, m0, n0, 0, tid);
+            load(g, A, B, M, N, K, lda, ldb, m0, n0, 0, tid);
             store(g, smem, smem + L::A_SZ, tid);
-            if (nkt > 1) load(g, A, B, M, N, K, m0, n0, BK, tid);
+            if (nkt > 1) load(g, A, B, M, N, K, lda, ldb, m0, n0, BK, tid);
             __syncthreads();
 
             float fa[2][FM][4], fb[2][FN][4];
@@ -243,7 +251,8 @@ struct MfmaGemm {
                         // while this tile's last MFMAs run.
                         float *nxt = smem + ((kt + 1) & 1) * L::STAGE;
                         if (kt + 1 < nkt) store(g, nxt, nxt + L::A_SZ, tid);
-                        if (kt + 2 < nkt) load(g, A, B, M, N, K, m0, n0, (kt + 2) * BK, tid);
+                        if (kt + 2 < nkt)
+                            load(g, A, B, M, N, K, lda, ldb, m0, n0, (kt + 2) * BK, tid);
                         __syncthreads();
                         if (kt + 1 < nkt)
                             fragments(nxt, nxt + L::A_SZ, 0, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
@@ -267,7 +276,10 @@ struct MfmaGemm {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (row < M) {
                         float *dst = C + (size_t)row * N + col;
-                        *dst = epilogue(acc[fi][fn][r], alpha, beta, dst);
+                        if (PARTIAL)
+                            *dst = acc[fi][fn][r];
+                        else
+                            *dst = epilogue(acc[fi][fn][r], alpha, beta, dst);
                     }
                 }
             }
@@ -284,9 +296,59 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
     const size_t z = blockIdx.y;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    MfmaGemm<TA, TB, Tile, VEC>::run(M, N, K, alpha, A + z * sA, B + z * sB,
-                                     beta, C + z * sC, tm * Tile::BM,
+    MfmaGemm<TA, TB, Tile, VEC>::run(M, N, K, TA ? M : K, TB ? K : N, alpha, A + z * sA,
+                                     B + z * sB, beta, C + z * sC, tm * Tile::BM,
                                      tn * Tile::BN, smem_dyn);
+}
+
+// Split-K: blockIdx.y = split s covers k in [s*kchunk, min(K, (s+1)*kchunk))
+// (kchunk a multiple of BK) and writes its raw fp32 sums to the M x N
+// partial P + s*M*N; splitk_reduce_k then adds the splits in order.
+template <bool TA, bool TB, class Tile, bool VEC>
+__global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
+    int M, int N, int K, const float *__restrict__ A, const float *__restrict__ B,
+    float *P, int tiles_m, int tiles_n, int kchunk) {
+    extern __shared__ float smem_dyn[];
+    const int s = blockIdx.y;
+    const int kb = s * kchunk;
+    const int klen = min(K, kb + kchunk) - kb;
+    int tm, tn;
+    group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    const float *As = TA ? A + (size_t)kb * M : A + kb;
+    const float *Bs = TB ? B + kb : B + (size_t)kb * N;
+    MfmaGemm<TA, TB, Tile, VEC>::template run<true>(
+        M, N, klen, TA ? M : K, TB ? K : N, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N,
+        tm * Tile::BM, tn * Tile::BN, smem_dyn);
+}
+
+// C = epilogue(sum_{s < splits} P[s], alpha, beta): one float4 of C per lane,
+// splits added in ascending order, so the result depends only on the shape.
+__global__ __launch_bounds__(256) void splitk_reduce_k(float *C, const float *P, int splits,
+                                                       long long mn, float alpha, float beta) {
+    const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    if (i + 3 < mn) {
+        float4 acc;
+        __builtin_memcpy(&acc, P + i, sizeof(acc));
+        for (int s = 1; s < splits; ++s) {
+            float4 v;
+            __builtin_memcpy(&v, P + (size_t)s * mn + i, sizeof(v));
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (beta != 0.0f) __builtin_memcpy(&c, C + i, sizeof(c));
+        c.x = epilogue(acc.x, alpha, beta, &c.x);
+        c.y = epilogue(acc.y, alpha, beta, &c.y);
+        c.z = epilogue(acc.z, alpha, beta, &c.z);
+        c.w = epilogue(acc.w, alpha, beta, &c.w);
+        __builtin_memcpy(C + i, &c, sizeof(c));
+    } else {
+        for (long long j = i; j < mn; ++j) {
+            float acc = P[j];
+            for (int s = 1; s < splits; ++s) acc += P[(size_t)s * mn + j];
+            C[j] = epilogue(acc, alpha, beta, &C[j]);
+        }
+    }
 }
 
 }  // namespace bmb

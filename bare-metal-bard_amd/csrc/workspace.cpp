@@ -3,15 +3,16 @@
 
 #include <hip/hip_runtime_api.h>
 
-#include <mutex>
 
 namespace bmb {
 
 namespace {
 constexpr int MAX_DEVICES = 64;
-std::mutex g_mu;
-void *g_ptr[MAX_DEVICES][SCRATCH_SLOTS] = {};
-size_t g_cap[MAX_DEVICES][SCRATCH_SLOTS] = {};
+// Per host thread: kernels a thread queues on the null stream run in its
+// order, so one thread's calls never overlap on its own buffers, and two
+// threads never share one.
+thread_local void *g_ptr[MAX_DEVICES][SCRATCH_SLOTS] = {};
+thread_local size_t g_cap[MAX_DEVICES][SCRATCH_SLOTS] = {};
 }  // namespace
 
 void *device_scratch(ScratchSlot slot, size_t bytes) {
@@ -19,7 +20,6 @@ void *device_scratch(ScratchSlot slot, size_t bytes) {
     if (slot < 0 || slot >= SCRATCH_SLOTS) return nullptr;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
     if (bytes == 0) bytes = 256;
-    std::lock_guard<std::mutex> lock(g_mu);
     void *&ptr = g_ptr[dev][slot];
     size_t &cap = g_cap[dev][slot];
     if (cap < bytes) {

@@ -12,12 +12,17 @@ the null stream, which is the stream the library launches on and torch's
 current stream, so `roofline.achieved` is the kernel's own average duration.
 
 The same JSON line also carries (none of them is `value`):
-  * config 1: N=1024, alpha=1, beta=0 for the VALU, MFMA and bf16x3 paths;
+  * config 1: N=1024, alpha=1, beta=0 for the VALU, MFMA and bf16x3 paths
+    (configs 1-3 are timed as bursts of back-to-back launches);
   * config 2: the square sweep N in {512 ... 8192} for the same three paths;
   * the ladder (ids 1-10) at N=4096;
   * config 3: gemm() at the GPT-2-small training shapes (BT=8192, C=768),
     forward NT, backward dX NN (beta 0) and dW TN (beta 1);
   * config 4: flash fwd+bwd at B=8, H=12, T=1024, d=64, with its roofline;
+  * config 5: the full GPT-2-small training step (12L/768/12H, T=1024, B=8,
+    V=50257 padded to 50304, fused attention, global-norm clipping, AdamW)
+    on synthetic uniform tokens: tokens/s over the timed steps and the loss
+    trajectory;
   * cpu_baseline: the oracle's order-preserving SGEMM and unfused attention
     on the host's cores (a bounded sample, reported, not a target).
 
@@ -51,7 +56,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ladder", action="store_true", help="skip the ladder, sweep and GPT shapes")
     ap.add_argument("--quick", action="store_true", help="headline SGEMM and flash only")
-    ap.add_argument("--only", choices=["sgemm", "flash"], default=None,
+    ap.add_argument("--only", choices=["sgemm", "flash", "gpt"], default=None,
                     help="run one workload only (for profiling)")
     ap.add_argument("--flash-sweep", action="store_true",
                     help="also time every forward and backward flash config (as the "
@@ -77,6 +82,24 @@ def timed(fn, steps, warmup):
         b.record()
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in ev]
+
+
+def timed_burst(fn, reps, warmup=2):
+    """Average duration (ms) of `reps` back-to-back launches between one pair
+    of HIP events: the throughput of a kernel in a stream, as the training
+    step runs it. Per-launch event pairs add a gap of tens of microseconds
+    around each launch, which distorts kernels of a few hundred microseconds."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
 
 
 def stats(ms):
@@ -199,7 +222,7 @@ def main():
     A = O.fill_xorshift(N * N, 0x12345678).reshape(N, N)
     Bm = O.fill_xorshift(N * N, 0x9ABCDEF0).reshape(N, N)
     C0 = O.fill_xorshift(N * N, 0x0F0F0F0F).reshape(N, N)
-    if args.only != "flash":
+    if args.only in (None, "sgemm"):
         smax = max(SWEEP_N) if extras else N
         dA = torch.from_numpy(O.fill_xorshift(smax * smax, 0x12345678)).cuda()
         dB = torch.from_numpy(O.fill_xorshift(smax * smax, 0x9ABCDEF0)).cuda()
@@ -236,9 +259,8 @@ def main():
             # Config 1: N=1024, alpha=1, beta=0.
             c1 = {}
             for kid in (8, 9, 10):
-                s1 = stats(timed(sq(kid, 1024, 1.0, 0.0), 20, 5))
-                c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3,
-                                                                          s1["median_ms"])
+                ms1 = timed_burst(sq(kid, 1024, 1.0, 0.0), 20, 5)
+                c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3, ms1)
             line["config1_n1024_gflops"] = c1
             # Config 2: square sweep, alpha=1, beta=0.5.
             sweep = {}
@@ -246,8 +268,7 @@ def main():
                 row = {}
                 for n in SWEEP_N:
                     reps = 10 if n <= 4096 else 5
-                    s2 = stats(timed(sq(kid, n), reps, 2))
-                    row[str(n)] = gf(2.0 * n ** 3, s2["median_ms"])
+                    row[str(n)] = gf(2.0 * n ** 3, timed_burst(sq(kid, n), reps))
                 sweep["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = row
             bmb.check("sgemm sweep")
             line["config2_sweep_gflops"] = sweep
@@ -266,14 +287,16 @@ def main():
             torch.cuda.empty_cache()
             line["config3_gpt_gemm_gflops"] = gpt_shapes(bmb, O, torch)
 
-    if args.only != "sgemm":
+    if args.only in (None, "flash"):
         line["flash"] = flash_bench(args, bmb, O, torch, traffic)
+    if args.only == "gpt" or (args.only is None and not args.quick):
+        line["config5_gpt_train_step"] = gpt_step_bench(args, bmb, torch)
 
     if not args.no_cpu and not args.quick:
         cpu = {}
-        if args.only != "flash":
+        if args.only in (None, "sgemm"):
             cpu = cpu_sgemm_baseline(O, A, Bm, C0, N)
-        if args.only != "sgemm":
+        if args.only in (None, "flash"):
             Bf, NH, T, hs = FLASH["B"], FLASH["NH"], FLASH["T"], FLASH["hs"]
             C = NH * hs
             qkv = O.fill_normal(Bf * T * 3 * C, 0xBEEF).reshape(Bf, T, 3 * C)
@@ -310,13 +333,99 @@ def gpt_shapes(bmb, O, torch):
                                1.0, w.data_ptr())
         reps = 3 if name == "lm_head" else 10
         res[name] = {"shape": "%dx%dx%d" % (BT, cout, cin),
-                     "fwd_NT": gf(fl, stats(timed(fwd, reps, 2))["median_ms"]),
-                     "dX_NN": gf(fl, stats(timed(dxf, reps, 2))["median_ms"]),
-                     "dW_TN_beta1": gf(fl, stats(timed(dwf, reps, 2))["median_ms"])}
+                     "fwd_NT": gf(fl, timed_burst(fwd, reps)),
+                     "dX_NN": gf(fl, timed_burst(dxf, reps)),
+                     "dW_TN_beta1": gf(fl, timed_burst(dwf, reps))}
         bmb.check("gemm " + name)
         del x, w, y
     torch.cuda.empty_cache()
     return res
+
+
+def lr_at(step, warmup, total, lr_max):
+    """The trainer's schedule (src/train_gpt.cu:233-238): linear warmup, then
+    cosine decay to lr_max / 10."""
+    import math
+    lr_min = lr_max * 0.1
+    if step <= warmup:
+        return lr_max * step / warmup
+    p = (step - warmup) / max(1, total - warmup)
+    return lr_min + 0.5 * (lr_max - lr_min) * (1.0 + math.cos(math.pi * p))
+
+
+def gpt_step_bench(args, bmb, torch):
+    """Config 5: one training step = gpt_forward + gpt_backward + global-norm
+    clipping + AdamW (src/train_gpt.cu:395-460 at one rank), GPT-2 small,
+    B=8, T=1024, random init N(0, 0.02) from gpt_init(1337), synthetic
+    i.i.d. uniform token ids in [0, 50257) (a fresh batch every step). Timed
+    on the host clock with the device synchronised at both ends; the step
+    itself blocks on the loss and the gradient norm, as the trainer's does."""
+    import numpy as np
+    cfg = (1024, 50257, 50304, 12, 12, 768)
+    B, T = 8, 1024
+    m = bmb.Model(cfg, B, T, use_flash=True)
+    m.init(1337)
+    n_params = int(m.g.num_params)
+    rng = np.random.default_rng(1337)
+    warm, steps = min(args.warmup, 3), args.steps
+    total = warm + steps
+    batches = [(rng.integers(0, cfg[1], B * T).astype(np.int32),
+                rng.integers(0, cfg[1], B * T).astype(np.int32)) for _ in range(total)]
+    L = bmb.lib()
+    losses, norms, times = [], [], []
+    for step in range(1, total + 1):
+        x, y = batches[step - 1]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loss = m.forward(x, y)
+        m.backward()
+        gn = L.grad_global_norm(m.g.grads_mem, n_params)
+        gs = 1.0 / gn if gn > 1.0 else 1.0
+        L.adamw_update(m.g.params_mem, m.g.grads_mem, m.g.m_mem, m.g.v_mem, n_params,
+                       lr_at(step, 100, 2000, 1e-3), 0.9, 0.999, 1e-8, 0.1, step, gs)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+        losses.append(loss)
+        norms.append(gn)
+    bmb.check("gpt step")
+    # one more step split into its phases, for the breakdown
+    x, y = batches[0]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.forward(x, y)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    m.backward()
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    gn = L.grad_global_norm(m.g.grads_mem, n_params)
+    L.adamw_update(m.g.params_mem, m.g.grads_mem, m.g.m_mem, m.g.v_mem, n_params, 1e-4, 0.9,
+                   0.999, 1e-8, 0.1, total + 1, 1.0)
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    m.free()
+    timed_ms = times[warm:]
+    ms = sum(timed_ms) / len(timed_ms)
+    hs = cfg[5] // cfg[4]
+    flops = 6.0 * B * T * n_params + 12.0 * cfg[3] * cfg[4] * T * T * hs * B
+    return {
+        "metric": "GPT-2 small training step tokens/s (fp32, AdamW)",
+        "value": round(B * T / (ms / 1e3), 1), "unit": "tokens/s",
+        "ms_per_step": round(ms, 3), "ms_best": round(min(timed_ms), 3),
+        "steps": steps, "warmup": warm,
+        "tflops_train_gpt_accounting": round(flops / (ms / 1e3) / 1e12, 2),
+        "pct_fp32_peak": round(100 * flops / (ms / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 1),
+        "phase_ms": {"forward": round((t1 - t0) * 1e3, 2), "backward": round((t2 - t1) * 1e3, 2),
+                     "norm_clip_adamw": round((t3 - t2) * 1e3, 2)},
+        "params": n_params,
+        "loss_first": round(losses[0], 5), "loss_last": round(losses[-1], 5),
+        "ln_V": round(float(np.log(cfg[1])), 5),
+        "grad_norm_first": round(norms[0], 5),
+        "config": {"workload": "GPT-2 small train step: 12L/768/12H, T=1024, B=8, V=50257 "
+                               "(Vp=50304), fused attention, grad clip 1.0, AdamW "
+                               "(0.9, 0.999, 1e-8, wd 0.1), lr schedule of train_gpt.cu",
+                   "flops_per_step": flops},
+    }
 
 
 def flash_bench(args, bmb, O, torch, traffic):

@@ -120,22 +120,43 @@ void orc_gemm_f32seq_mt(int ta, int tb, int M, int N, int K, float alpha,
 void orc_gemm_f64(int ta, int tb, int M, int N, int K, double alpha,
                   const float *A, const float *B, double beta, const float *C0,
                   double *Cout) {
-    double *acc = (double *)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
-    for (int i = 0; i < M; ++i) {
-        for (int j = 0; j < N; ++j) acc[j] = 0.0;
-        for (int k = 0; k < K; ++k) {
-            const double a = (double)elemA(ta, A, M, K, i, k);
-            for (int j = 0; j < N; ++j)
-                acc[j] += a * (double)elemB(tb, B, N, K, k, j);
+    /* Rows are independent: OpenMP over i (each row is computed by one
+     * thread, so the result does not depend on the thread count). Row i of
+     * op(A) is widened into a contiguous buffer; with transB the j-th output
+     * is then a dot product of two k-contiguous rows, otherwise the k loop
+     * streams rows of B -- both cache friendly whatever the transposes. */
+#pragma omp parallel
+    {
+        double *acc = (double *)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+        double *arow = (double *)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int i = 0; i < M; ++i) {
+            for (int k = 0; k < K; ++k) arow[k] = (double)elemA(ta, A, M, K, i, k);
+            if (tb) {
+                for (int j = 0; j < N; ++j) {
+                    const float *brow = B + (size_t)j * K;
+                    double d = 0.0;
+                    for (int k = 0; k < K; ++k) d += arow[k] * (double)brow[k];
+                    acc[j] = d;
+                }
+            } else {
+                for (int j = 0; j < N; ++j) acc[j] = 0.0;
+                for (int k = 0; k < K; ++k) {
+                    const double a = arow[k];
+                    const float *brow = B + (size_t)k * N;
+                    for (int j = 0; j < N; ++j) acc[j] += a * (double)brow[j];
+                }
+            }
+            for (int j = 0; j < N; ++j) {
+                const size_t idx = (size_t)i * N + j;
+                double c = alpha * acc[j];
+                if (beta != 0.0) c += beta * (double)C0[idx];
+                Cout[idx] = c;
+            }
         }
-        for (int j = 0; j < N; ++j) {
-            const size_t idx = (size_t)i * N + j;
-            double c = alpha * acc[j];
-            if (beta != 0.0) c += beta * (double)C0[idx];
-            Cout[idx] = c;
-        }
+        free(acc);
+        free(arow);
     }
-    free(acc);
 }
 
 void orc_batched_gemm_f32seq(int ta, int tb, int batch, int M, int N, int K,

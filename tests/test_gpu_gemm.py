@@ -106,3 +106,75 @@ def test_gpt_training_shapes(gpu, g):
     err, bad = O.normwise(got[rows], ref)
     print("  normwise %.2e" % err)
     assert bad == 0 and err < 1e-4
+
+
+# Shapes whose output-tile count is small against their K: gemm() splits K
+# into ranges, sums each into a scratch partial and adds the partials in range
+# order (deterministic). Odd K leaves a short last range.
+SPLIT = [(1000, 1000, 1001), (257, 129, 3000), (96, 160, 777), (1, 1, 4096), (3, 300, 5000),
+         (768, 768, 8192)]
+
+
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("shape", SPLIT, ids=lambda s: "%dx%dx%d" % s)
+def test_split_k(gpu, shape, trans):
+    import torch
+    M, N, K = shape
+    ta, tb = trans
+    A = O.fill_xorshift(M * K, 0x1357)
+    B = O.fill_xorshift(K * N, 0x2468)
+    C0 = O.fill_xorshift(M * N, 0x9999)
+    dA, dB = dev(A), dev(B)
+    print("split-k %s M=%d N=%d K=%d" % (_tag(trans), M, N, K), flush=True)
+    # beta = 0: C is write-only, so NaN in it must not reach the result
+    gC = Guarded(M * N, fill=np.full(M * N, np.nan, np.float32))
+    bmb.gemm(ta, tb, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 0.0, gC.ptr)
+    sync("gemm beta 0")
+    assert gC.ok()
+    ref0 = O.gemm_f64(ta, tb, M, N, K, 0.75, A, B, 0.0, None)
+    err, bad = O.normwise(gC.get(), ref0)
+    assert bad == 0 and err < fp32_order_bound(K), err
+    # beta != 0, twice: bit-identical
+    outs = []
+    for _ in range(2):
+        g2 = Guarded(M * N, fill=C0)
+        bmb.gemm(ta, tb, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 1.25, g2.ptr)
+        sync("gemm")
+        assert g2.ok()
+        outs.append(g2.get())
+    assert np.array_equal(outs[0], outs[1])
+    ref = O.gemm_f64(ta, tb, M, N, K, 0.75, A, B, 1.25, C0)
+    err, bad = O.normwise(outs[0], ref)
+    assert bad == 0 and err < fp32_order_bound(K), err
+    # operands one float off 16-byte alignment (the 32-bit load path)
+    mA = torch.zeros(A.size + 1, device="cuda")
+    mB = torch.zeros(B.size + 1, device="cuda")
+    mC = torch.zeros(C0.size + 1, device="cuda")
+    mA[1:].copy_(dA)
+    mB[1:].copy_(dB)
+    mC[1:].copy_(dev(C0))
+    bmb.gemm(ta, tb, M, N, K, 0.75, mA[1:].data_ptr(), mB[1:].data_ptr(), 1.25, mC[1:].data_ptr())
+    sync("gemm misaligned")
+    err, bad = O.normwise(mC[1:].cpu().numpy(), ref)
+    assert bad == 0 and err < fp32_order_bound(K), err
+
+
+def test_non_null_stream_matches(gpu):
+    """On a stream other than the null stream gemm() does not split K (its
+    scratch is ordered by the null stream only); the result agrees with the
+    oracle all the same."""
+    import torch
+    M, N, K = 384, 384, 4096
+    A = O.fill_xorshift(M * K, 0x1111)
+    B = O.fill_xorshift(K * N, 0x2222)
+    C0 = O.fill_xorshift(M * N, 0x3333)
+    dA, dB, dC = dev(A), dev(B), dev(C0)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        bmb.gemm(True, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr(),
+                 s.cuda_stream)
+    s.synchronize()
+    bmb.check("gemm on stream")
+    ref = O.gemm_f64(True, False, M, N, K, 1.0, A, B, 0.5, C0)
+    err, bad = O.normwise(dC.cpu().numpy(), ref)
+    assert bad == 0 and err < fp32_order_bound(K)
