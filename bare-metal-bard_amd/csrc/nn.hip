@@ -66,7 +66,7 @@ inline unsigned grid_for(long long items) {
 // 4*(i % C4) .. +3, with C4 = ceil(C/4). VEC: C % 4 == 0, so every chunk is
 // whole and rows are 4-byte aligned for the 128-bit accesses.
 
-// out[r, c] = wte[tok[r], c] + wpe[r % T, c]   (src/nn.cu:22-35)
+// out[r, c] = wte[tok[r], c] + wpe[r % T, c]   (src/nn.cu:23-36)
 template <bool VEC>
 __global__ __launch_bounds__(NT) void encoder_fwd_k(float *out, const int *tokens,
                                                      const float *wte, const float *wpe,
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(NT) void encoder_bwd_wte_k(float *dwte, const float
 // ------------------------------------------------------------------ layernorm
 // One wave per row, the row held in NCH float4 registers per lane
 // (C <= 256*NCH, C % 4 == 0). Mean first, then the variance about it
-// (src/nn.cu:55-82): biased, eps 1e-5.
+// (src/nn.cu:54-82): biased, eps 1e-5.
 template <int NCH>
 __global__ __launch_bounds__(NT) void ln_fwd_k(float *out, float *mean, float *rstd,
                                                 const float *inp, const float *weight,
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(NT) void ln_fwd_generic_k(float *out, float *mean, 
 
 // Layernorm backward, fused (C % 4 == 0, C <= 256*NCH). A workgroup of
 // LN_WAVES waves owns rows [blk*rpb, (blk+1)*rpb); each wave takes every
-// LN_WAVES-th of them. Per row (src/nn.cu:90-111):
+// LN_WAVES-th of them. Per row (src/nn.cu:85-111):
 //   dinp += rstd * (dxhat - mean(dxhat) - xhat * mean(dxhat * xhat)),
 //   dxhat = dout * w, xhat = (x - mean) * rstd.
 // The weight and bias gradients of the workgroup's rows are summed in
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(NT) void colsum_finish_k(float *dst0, float *dst1, 
 }
 
 // ------------------------------------------------------------ elementwise ops
-// GPT-2's tanh GELU (src/nn.cu:116-142).
+// GPT-2's tanh GELU (src/nn.cu:116-151).
 constexpr float GELU_S = 0.7978845608028654f;  // sqrt(2/pi)
 constexpr float GELU_C = 0.044715f;
 
@@ -483,7 +483,7 @@ struct Zero {
     __device__ void one(long long i) const { p[i] = 0.0f; }
 };
 
-// AdamW (src/nn.cu:300-319) with the reference's fp32 operation order. FP
+// AdamW (src/nn.cu:240-255, 336-343) with the reference's fp32 operation order. FP
 // contraction is off here so that each product and sum rounds separately, as
 // written; the result is then a function of the inputs alone.
 __device__ __forceinline__ void adam1(float &p, float &m, float &v, float grad, float lr,
@@ -579,7 +579,7 @@ __global__ __launch_bounds__(NT) void xent_bwd_k(float *dlogits, const float *pr
 // One workgroup of NTHR lanes per row, the row's first V logits held in NCH
 // float4 registers per lane (V <= 4*NTHR*NCH, Vp % 4 == 0): max, then
 // exp(x - max) and its sum, then the normalised probabilities -- one read of
-// the logits and one write of the probabilities (src/nn.cu:177-203).
+// the logits and one write of the probabilities (src/nn.cu:197-221).
 // exp(x - m) is exp2((x - m) * log2 e) on v_exp_f32.
 template <int NTHR>
 __device__ __forceinline__ float block_reduce(float v, float *sh, bool is_max) {

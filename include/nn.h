@@ -6,17 +6,18 @@
  * so N = B*T. Weights are (out_features, in_features). All pointers are
  * caller-owned device pointers; launches go to the null stream. Names,
  * argument order and meaning follow src/nn.h:10-60. Where the reference
- * silently relies on n % 4 == 0 or C % 4 == 0 (src/nn.cu:230-248) these
+ * silently relies on n % 4 == 0 or C % 4 == 0 (src/nn.cu:304-322) these
  * entry points also handle the remainder.
  *
  * Determinism: every reduction here runs in a fixed order that depends only
  * on the shape, so repeated calls on the same inputs give the same bits. The
- * reference uses atomics for the layernorm, bias and embedding gradients
- * (src/nn.cu:44-45,108-109); this library reduces those through per-block
- * partial sums in a library-owned per-device scratch buffer (a few MB at
- * GPT-2 sizes, allocated on first use and kept until the process ends) and,
- * for the token-embedding gradient, by letting the first position of each
- * token id sum all its positions in order.
+ * reference uses atomics for the layernorm weight/bias and the embedding
+ * gradients (src/nn.cu:44-45,108-109); this library reduces the layernorm and
+ * bias gradients through per-block partial sums in a library-owned scratch
+ * buffer (per host thread and device; a few MB at GPT-2 sizes, allocated on
+ * first use and kept until the process ends) and the token-embedding
+ * gradient by letting the first position of each token id sum all its
+ * positions in order.
  */
 #ifndef BMB_NN_H
 #define BMB_NN_H
@@ -79,7 +80,7 @@ void crossentropy_softmax_backward(float *dlogits, const float *probs,
 /* ---- optimizer (src/nn.h:53-57) ----
  * AdamW with bias correction (1 - beta^step, computed on the host in fp32)
  * and decoupled weight decay; every gradient is multiplied by grad_scale on
- * the way in. Same fp32 operation order as src/nn.cu:306-318. */
+ * the way in. Same fp32 operation order as src/nn.cu:240-255. */
 void adamw_update(float *params, float *grads, float *m, float *v, int n,
                   float lr, float beta1, float beta2, float eps,
                   float weight_decay, int step, float grad_scale);

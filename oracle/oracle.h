@@ -109,37 +109,37 @@ void orc_attn_fwdbwd_f32(const float *qkv, const float *dout, int B, int T,
 /* ---- transformer building blocks (oracle_gpt.c) ---------------------------
  * fp64 in, fp64 out; the fp32 values the GPU sees are widened exactly.
  * Gradient outputs marked "+=" accumulate, as the reference's do. */
-/* out[b,t,:] = wte[tokens[b,t],:] + wpe[t,:]  (src/nn.cu:22-35) */
+/* out[b,t,:] = wte[tokens[b,t],:] + wpe[t,:]  (src/nn.cu:23-36) */
 void orc_encoder_fwd(double *out, const int *tokens, const double *wte,
                      const double *wpe, int B, int T, int C);
-/* dwte[tok,:] += dout[b,t,:], dwpe[t,:] += dout[b,t,:]  (src/nn.cu:37-46) */
+/* dwte[tok,:] += dout[b,t,:], dwpe[t,:] += dout[b,t,:]  (src/nn.cu:38-46) */
 void orc_encoder_bwd(double *dwte, double *dwpe, const double *dout,
                      const int *tokens, int B, int T, int C);
-/* biased variance, eps 1e-5, rstd = 1/sqrt(var + eps)  (src/nn.cu:55-82) */
+/* biased variance, eps 1e-5, rstd = 1/sqrt(var + eps)  (src/nn.cu:54-82) */
 void orc_layernorm_fwd(double *out, double *mean, double *rstd,
                        const double *inp, const double *w, const double *b,
                        int N, int C);
 /* dinp += rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)), dw += dy xhat,
- * db += dy  (src/nn.cu:90-111) */
+ * db += dy  (src/nn.cu:85-111) */
 void orc_layernorm_bwd(double *dinp, double *dw, double *db,
                        const double *dout, const double *inp, const double *w,
                        const double *mean, const double *rstd, int N, int C);
-/* GPT-2 tanh GELU and its derivative (src/nn.cu:116-142); dinp written */
+/* GPT-2 tanh GELU and its derivative (src/nn.cu:116-151); dinp written */
 void orc_gelu_fwd(double *out, const double *inp, size_t n);
 void orc_gelu_bwd(double *dinp, const double *inp, const double *dout, size_t n);
-/* dbias[c] += sum_r dout[r,c]  (src/nn.cu:168-175) */
+/* dbias[c] += sum_r dout[r,c]  (src/nn.cu:184-192) */
 void orc_bias_bwd(double *dbias, const double *dout, int N, int C);
 /* softmax over the first V of Vp columns, probs[V:Vp] = 0, loss =
- * -ln(max(p[target], 1e-30)) (src/nn.cu:177-203); a target outside [0,Vp)
+ * -ln(max(p[target], 1e-30)) (src/nn.cu:197-221); a target outside [0,Vp)
  * gives NaN. losses may be NULL. */
 void orc_softmax_xent_fwd(double *probs, double *losses, const double *logits,
                           const int *targets, int N, int V, int Vp);
 /* dlogits = (p - [i == target]) * scale for i < V, 0 beyond
- * (src/nn.cu:208-219) */
+ * (src/nn.cu:226-236) */
 void orc_xent_bwd(double *dlogits, const double *probs, const int *targets,
                   int N, int V, int Vp, double scale);
-/* fp32 AdamW restated operation by operation (src/nn.cu:300-319, bias
- * corrections 1 - powf(beta, step) as at src/nn.cu:326-329). */
+/* fp32 AdamW restated operation by operation (src/nn.cu:240-255, bias
+ * corrections 1 - powf(beta, step) as at src/nn.cu:336-343). */
 void orc_adamw_f32(float *params, const float *grads, float *m, float *v,
                    size_t n, float lr, float beta1, float beta2, float eps,
                    float wd, int step, float grad_scale);

@@ -48,7 +48,7 @@ def test_layernorm_matches_torch():
     assert np.allclose(mean, x.mean(1), atol=1e-14)
     assert np.allclose(rstd, 1 / np.sqrt(x.var(1) + 1e-5), rtol=1e-13)
     yt.backward(torch.tensor(dy))
-    # accumulate onto non-zero buffers (src/nn.cu:107-109 use +=)
+    # accumulate onto non-zero buffers (src/nn.cu:106-109 use +=)
     d0, w0, b0 = r.standard_normal((N, C)), r.standard_normal(C), r.standard_normal(C)
     dinp, dw, db = O.layernorm_bwd(d0, w0, b0, dy, x, w, mean, rstd, N, C)
     assert np.abs(dinp - d0 - xt.grad.numpy()).max() < 1e-12
