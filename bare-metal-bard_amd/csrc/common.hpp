@@ -28,6 +28,21 @@ __device__ __forceinline__ float epilogue(float acc, float alpha, float beta,
     return beta == 0.0f ? alpha * acc : fma_rn(alpha, acc, beta * (*c));
 }
 
+// GPT-2's tanh GELU (src/nn.cu:116-121) and its derivative (:132-139),
+// shared by gelu_forward/backward and the fused GEMM epilogue so that both
+// produce the same bits.
+constexpr float GELU_S = 0.7978845608028654f;  // sqrt(2/pi)
+constexpr float GELU_C = 0.044715f;
+__device__ __forceinline__ float gelu(float x) {
+    return 0.5f * x * (1.0f + tanhf(GELU_S * (x + GELU_C * x * x * x)));
+}
+__device__ __forceinline__ float gelu_grad(float x, float g) {
+    const float t = tanhf(GELU_S * (x + GELU_C * x * x * x));
+    const float sech2 = 1.0f - t * t;
+    const float dinner = GELU_S * (1.0f + 3.0f * GELU_C * x * x);
+    return g * (0.5f * (1.0f + t) + 0.5f * x * sech2 * dinner);
+}
+
 // 128-bit global/LDS moves.
 __device__ __forceinline__ float4 ld4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);

@@ -14,6 +14,7 @@
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
 #include "../../include/kernels.h"
+#include "gemm_fused.hpp"
 #include "launch.hpp"
 #include "workspace.hpp"
 
@@ -125,31 +126,31 @@ Plan pick(int M, int N, int K, int batch, bool may_split) {
     return best;
 }
 
-template <bool TA, bool TB, class Tile>
+template <bool TA, bool TB, class Tile, int EPI>
 void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
                  long long sA, const float *B, long long sB, float beta,
-                 float *C, long long sC, hipStream_t stream, bool vec) {
+                 float *C, long long sC, hipStream_t stream, bool vec, bmb::EpiArgs ep) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, batch);
     if (vec) {
-        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true>, L::SMEM_BYTES);
-        bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
+        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, L::SMEM_BYTES);
+        bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
-                    sC, tiles_m, tiles_n);
+                    sC, tiles_m, tiles_n, ep);
     } else {
-        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false>, L::SMEM_BYTES);
-        bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
+        bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, L::SMEM_BYTES);
+        bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
-                    sC, tiles_m, tiles_n);
+                    sC, tiles_m, tiles_n, ep);
     }
 }
 
 // Split-K: the partial sums of each K range go to P (splits x M x N), then
-// one reduce kernel adds them in range order and applies alpha / beta.
-template <bool TA, bool TB, class Tile>
+// one reduce kernel adds them in range order and applies the epilogue.
+template <bool TA, bool TB, class Tile, int EPI>
 void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *A,
-                  const float *B, float beta, float *C, float *P, bool vec) {
+                  const float *B, float beta, float *C, float *P, bool vec, bmb::EpiArgs ep) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, p.splits);
@@ -163,16 +164,16 @@ void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *
                     L::SMEM_BYTES, nullptr, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
     }
     const long long mn = (long long)M * N;
-    bmb::launch(bmb::splitk_reduce_k, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
-                nullptr, C, (const float *)P, p.splits, mn, alpha, beta);
+    bmb::launch(bmb::splitk_reduce_k<EPI>, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
+                nullptr, C, (const float *)P, p.splits, mn, N, alpha, beta, ep);
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int EPI = bmb::EPI_BLAS>
 void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
               long long sA, const float *B, long long sB, float beta, float *C,
-              long long sC, hipStream_t stream) {
+              long long sC, hipStream_t stream, bmb::EpiArgs ep = {}) {
     if (M <= 0 || N <= 0 || batch <= 0) return;
     // 128-bit loads need the contiguous axis of each stored operand to be a
     // multiple of 4 floats, 16-byte aligned bases, and batch strides that keep
@@ -189,25 +190,25 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     }
     if (p.splits > 1) {
         switch (p.tile.kind) {
-        case TileKind::L: launch_split<TA, TB, TileL>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
-        case TileKind::M: launch_split<TA, TB, TileM>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
-        case TileKind::N: launch_split<TA, TB, TileN>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
-        case TileKind::S: launch_split<TA, TB, TileS>(p, M, N, K, alpha, A, B, beta, C, P, vec); break;
+        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
+        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
+        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
+        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
         }
         return;
     }
     switch (p.tile.kind) {
     case TileKind::L:
-        launch_tile<TA, TB, TileL>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     case TileKind::M:
-        launch_tile<TA, TB, TileM>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     case TileKind::N:
-        launch_tile<TA, TB, TileN>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     case TileKind::S:
-        launch_tile<TA, TB, TileS>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec);
+        launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     }
 }
@@ -222,6 +223,16 @@ void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
 }
 
 }  // namespace
+
+void bmb::gemm_bias_nt(int M, int N, int K, const float *A, const float *W, const float *bias,
+                       float *C, float *gelu_out) {
+    if (gelu_out != nullptr)
+        dispatch<false, true, bmb::EPI_BIAS_GELU>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0,
+                                                  nullptr, bmb::EpiArgs{bias, gelu_out});
+    else
+        dispatch<false, true, bmb::EPI_BIAS>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0, nullptr,
+                                             bmb::EpiArgs{bias, nullptr});
+}
 
 extern "C" {
 

@@ -42,6 +42,35 @@ namespace bmb {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// What the epilogue does with a finished fp32 sum `acc` of output (row, col).
+enum Epi {
+    EPI_BLAS = 0,       // C = alpha * acc + beta * C (beta == 0: C write-only)
+    EPI_PARTIAL = 1,    // C = acc (a split-K partial)
+    EPI_BIAS = 2,       // C = acc + bias[col]
+    EPI_BIAS_GELU = 3,  // C = acc + bias[col] and act = gelu(C), both stored
+};
+struct EpiArgs {
+    const float *bias;  // EPI_BIAS*: N floats
+    float *act;         // EPI_BIAS_GELU: M x N, same layout as C
+};
+
+// The fused epilogues are the reference's separate passes in one: gemm with
+// alpha = 1, beta = 0 stores acc, bias_forward adds bias[col] (one rounding),
+// gelu_forward maps the sum (src/gpt.cu:256-277) -- the same fp32 results.
+template <int EPI>
+__device__ __forceinline__ void store_out(float *C, float *act, size_t idx, float acc,
+                                          float alpha, float beta, float bias) {
+    if (EPI == EPI_PARTIAL) {
+        C[idx] = acc;
+    } else if (EPI == EPI_BLAS) {
+        C[idx] = epilogue(acc, alpha, beta, C + idx);
+    } else {
+        const float v = acc + bias;
+        C[idx] = v;
+        if (EPI == EPI_BIAS_GELU) act[idx] = gelu(v);
+    }
+}
+
 template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
 struct MfmaTile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
@@ -205,15 +234,14 @@ struct MfmaGemm {
 
     // One output tile (m0, n0) of one problem over k in [0, K); A and B are
     // positioned at k = 0 of that range, lda / ldb are their row strides.
-    // smem holds two stages. PARTIAL: store the raw fp32 sums to C (an
-    // M x N split-K partial) instead of applying the alpha/beta epilogue.
-    template <bool PARTIAL = false>
+    // smem holds two stages. EPI selects what is stored (see Epi).
+    template <int EPI = EPI_BLAS>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
                                                float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B,
                                                float beta, float *C, int m0,
-                                               int n0, float *smem) {
+                                               int n0, float *smem, EpiArgs ep = {}) {
         constexpr int G = BK / 8;  // 8-k groups per tile (even)
         const int tid = threadIdx.x;
         const int wave = tid >> 6, lane = tid & 63;
@@ -271,34 +299,32 @@ struct MfmaGemm {
             for (int fn = 0; fn < FN; ++fn) {
                 const int col = n0 + wn + fn * 32 + l32;
                 if (col >= N) continue;
+                const float bias = (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) ? ep.bias[col] : 0.0f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (row < M) {
-                        float *dst = C + (size_t)row * N + col;
-                        if (PARTIAL)
-                            *dst = acc[fi][fn][r];
-                        else
-                            *dst = epilogue(acc[fi][fn][r], alpha, beta, dst);
-                    }
+                    if (row < M)
+                        store_out<EPI>(C, ep.act, (size_t)row * N + col, acc[fi][fn][r], alpha,
+                                       beta, bias);
                 }
             }
     }
 };
 
-// Grid: x = output tiles (XCD-remapped, grouped), y = batch index.
-template <bool TA, bool TB, class Tile, bool VEC>
+// Grid: x = output tiles (XCD-remapped, grouped), y = batch index. The
+// fused epilogues (EPI_BIAS*) are used for single problems only.
+template <bool TA, bool TB, class Tile, bool VEC, int EPI>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
     int M, int N, int K, float alpha, const float *__restrict__ A,
     long long sA, const float *__restrict__ B, long long sB, float beta,
-    float *C, long long sC, int tiles_m, int tiles_n) {
+    float *C, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
     extern __shared__ float smem_dyn[];
     const size_t z = blockIdx.y;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    MfmaGemm<TA, TB, Tile, VEC>::run(M, N, K, TA ? M : K, TB ? K : N, alpha, A + z * sA,
-                                     B + z * sB, beta, C + z * sC, tm * Tile::BM,
-                                     tn * Tile::BN, smem_dyn);
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, TA ? M : K, TB ? K : N, alpha,
+                                                   A + z * sA, B + z * sB, beta, C + z * sC,
+                                                   tm * Tile::BM, tn * Tile::BN, smem_dyn, ep);
 }
 
 // Split-K: blockIdx.y = split s covers k in [s*kchunk, min(K, (s+1)*kchunk))
@@ -316,38 +342,53 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const float *As = TA ? A + (size_t)kb * M : A + kb;
     const float *Bs = TB ? B + kb : B + (size_t)kb * N;
-    MfmaGemm<TA, TB, Tile, VEC>::template run<true>(
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI_PARTIAL>(
         M, N, klen, TA ? M : K, TB ? K : N, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N,
         tm * Tile::BM, tn * Tile::BN, smem_dyn);
 }
 
-// C = epilogue(sum_{s < splits} P[s], alpha, beta): one float4 of C per lane,
-// splits added in ascending order, so the result depends only on the shape.
+// C = epilogue of sum_{s < splits} P[s]: one float4 of C per lane, splits
+// added in ascending order, so the result depends only on the shape. N is
+// the row length (for the bias column of an element).
+template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_k(float *C, const float *P, int splits,
-                                                       long long mn, float alpha, float beta) {
+                                                       long long mn, int N, float alpha,
+                                                       float beta, EpiArgs ep) {
     const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
-    if (i + 3 < mn) {
-        float4 acc;
-        __builtin_memcpy(&acc, P + i, sizeof(acc));
+    const bool whole = i + 3 < mn;
+    float acc[4];
+    if (whole) {
+        float4 v;
+        __builtin_memcpy(&v, P + i, sizeof(v));
+        acc[0] = v.x; acc[1] = v.y; acc[2] = v.z; acc[3] = v.w;
         for (int s = 1; s < splits; ++s) {
-            float4 v;
             __builtin_memcpy(&v, P + (size_t)s * mn + i, sizeof(v));
-            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;
         }
+    } else {
+        for (int k = 0; k < 4; ++k) {
+            acc[k] = 0.0f;
+            if (i + k < mn) {
+                acc[k] = P[i + k];
+                for (int s = 1; s < splits; ++s) acc[k] += P[(size_t)s * mn + i + k];
+            }
+        }
+    }
+    if (EPI == EPI_BLAS && whole) {
         float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
         if (beta != 0.0f) __builtin_memcpy(&c, C + i, sizeof(c));
-        c.x = epilogue(acc.x, alpha, beta, &c.x);
-        c.y = epilogue(acc.y, alpha, beta, &c.y);
-        c.z = epilogue(acc.z, alpha, beta, &c.z);
-        c.w = epilogue(acc.w, alpha, beta, &c.w);
+        c.x = epilogue(acc[0], alpha, beta, &c.x);
+        c.y = epilogue(acc[1], alpha, beta, &c.y);
+        c.z = epilogue(acc[2], alpha, beta, &c.z);
+        c.w = epilogue(acc[3], alpha, beta, &c.w);
         __builtin_memcpy(C + i, &c, sizeof(c));
-    } else {
-        for (long long j = i; j < mn; ++j) {
-            float acc = P[j];
-            for (int s = 1; s < splits; ++s) acc += P[(size_t)s * mn + j];
-            C[j] = epilogue(acc, alpha, beta, &C[j]);
-        }
+        return;
+    }
+    for (int k = 0; k < 4; ++k) {
+        if (i + k >= mn) break;
+        const float bias = EPI == EPI_BLAS ? 0.0f : ep.bias[(i + k) % N];
+        store_out<EPI>(C, ep.act, (size_t)(i + k), acc[k], alpha, beta, bias);
     }
 }
 

@@ -21,6 +21,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "nn_fused.hpp"
 #include "workspace.hpp"
 #include "../../include/nn.h"
 
@@ -167,11 +168,14 @@ __global__ __launch_bounds__(NT) void encoder_bwd_wte_k(float *dwte, const float
 // ------------------------------------------------------------------ layernorm
 // One wave per row, the row held in NCH float4 registers per lane
 // (C <= 256*NCH, C % 4 == 0). Mean first, then the variance about it
-// (src/nn.cu:54-82): biased, eps 1e-5.
-template <int NCH>
+// (src/nn.cu:54-82): biased, eps 1e-5. RES: the row is first formed as
+// res_a + res_b and stored to res_out (residual_forward fused in front: the
+// same one rounding per element, then the same layernorm of the stored sum).
+template <int NCH, bool RES>
 __global__ __launch_bounds__(NT) void ln_fwd_k(float *out, float *mean, float *rstd,
                                                 const float *inp, const float *weight,
-                                                const float *bias, int N, int C) {
+                                                const float *bias, int N, int C,
+                                                float *res_out, const float *res_b) {
     const int row = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= N) return;
@@ -182,6 +186,11 @@ __global__ __launch_bounds__(NT) void ln_fwd_k(float *out, float *mean, float *r
     for (int k = 0; k < NCH; ++k) {
         const int c = (k * 64 + lane) * 4;
         v[k] = c < C ? ldu4(x + c) : zero4();
+        if (RES && c < C) {
+            const float4 y = ldu4(res_b + (size_t)row * C + c);
+            v[k] = make_float4(v[k].x + y.x, v[k].y + y.y, v[k].z + y.z, v[k].w + y.w);
+            stu4(res_out + (size_t)row * C + c, v[k]);
+        }
         s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
     }
     const float mu = wave_sum(s) / (float)C;
@@ -407,19 +416,8 @@ __global__ __launch_bounds__(NT) void colsum_finish_k(float *dst0, float *dst1, 
 }
 
 // ------------------------------------------------------------ elementwise ops
-// GPT-2's tanh GELU (src/nn.cu:116-151).
-constexpr float GELU_S = 0.7978845608028654f;  // sqrt(2/pi)
-constexpr float GELU_C = 0.044715f;
-
-__device__ __forceinline__ float gelu1(float x) {
-    return 0.5f * x * (1.0f + tanhf(GELU_S * (x + GELU_C * x * x * x)));
-}
-__device__ __forceinline__ float dgelu1(float x, float g) {
-    const float t = tanhf(GELU_S * (x + GELU_C * x * x * x));
-    const float sech2 = 1.0f - t * t;
-    const float dinner = GELU_S * (1.0f + 3.0f * GELU_C * x * x);
-    return g * (0.5f * (1.0f + t) + 0.5f * x * sech2 * dinner);
-}
+__device__ __forceinline__ float gelu1(float x) { return bmb::gelu(x); }
+__device__ __forceinline__ float dgelu1(float x, float g) { return bmb::gelu_grad(x, g); }
 
 // Flat elementwise map: work item i covers elements 4i .. 4i+3 (the last one
 // may be partial); a grid-stride loop keeps the launch under the 2^32
@@ -762,11 +760,12 @@ void colsum_finish(float *d0, float *d1, int C0, const float *partial, int G, in
                 partial, G, width);
 }
 
-template <int NCH>
+template <int NCH, bool RES = false>
 void ln_fwd_launch(float *out, float *mean, float *rstd, const float *inp, const float *w,
-                   const float *b, int N, int C) {
-    bmb::launch(ln_fwd_k<NCH>, dim3(ceil_div(N, NT / 64)), dim3(NT), 0, nullptr, out, mean,
-                rstd, inp, w, b, N, C);
+                   const float *b, int N, int C, float *res_out = nullptr,
+                   const float *res_b = nullptr) {
+    bmb::launch(ln_fwd_k<NCH, RES>, dim3(ceil_div(N, NT / 64)), dim3(NT), 0, nullptr, out, mean,
+                rstd, inp, w, b, N, C, res_out, res_b);
 }
 
 template <int NCH>
@@ -794,6 +793,21 @@ float scalar_result(const float *dptr) {
 }
 
 }  // namespace
+
+void bmb::residual_layernorm_forward(float *res_out, float *ln_out, float *mean, float *rstd,
+                                     const float *a, const float *b, const float *weight,
+                                     const float *bias, int N, int C) {
+    if (N <= 0 || C <= 0) return;
+    switch (row_chunks(C)) {
+        case 1: return ln_fwd_launch<1, true>(ln_out, mean, rstd, a, weight, bias, N, C, res_out, b);
+        case 2: return ln_fwd_launch<2, true>(ln_out, mean, rstd, a, weight, bias, N, C, res_out, b);
+        case 3: return ln_fwd_launch<3, true>(ln_out, mean, rstd, a, weight, bias, N, C, res_out, b);
+        case 4: return ln_fwd_launch<4, true>(ln_out, mean, rstd, a, weight, bias, N, C, res_out, b);
+        default:
+            residual_forward(res_out, a, b, N * C);
+            layernorm_forward(ln_out, mean, rstd, res_out, weight, bias, N, C);
+    }
+}
 
 extern "C" {
 

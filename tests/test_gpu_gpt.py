@@ -258,3 +258,64 @@ def test_gpt2_small_first_step(gpu):
     assert abs(l1 - math.log(cfg[1])) < 0.5
     assert np.isfinite(gn1) and gn1 > 0
     assert l1 == l2 and gn1 == gn2
+
+
+def test_fused_forward_matches_separate_ops(gpu):
+    """gpt_forward fuses bias (and GELU) into the GEMM epilogue and each
+    residual add into the following layernorm. Recompute layer 0 and the start
+    of layer 1 from the stored activations with the reference's separate
+    launches (gemm, bias_forward, gelu_forward, residual_forward,
+    layernorm_forward, src/gpt.cu:254-283): every tensor must be bit-identical."""
+    import torch
+    m = _model(True)
+    x, y = _batch(31)
+    m.forward(x, y)
+    sync("forward")
+    C, N = CFG[5], B * T
+    off = _offsets()
+    p = _params(m)
+    P = {n: p[off[t]:off[t + 1]] for t, n in enumerate(O.PARAM_NAMES)}
+    a = m.g.acts
+    get = lambda ptr, n, o=0: d2h(ptr + 4 * o, n)
+    ln1, qkv = get(a.ln1, N * C), get(a.qkv, N * 3 * C)
+    atty, attproj = get(a.atty, N * C), get(a.attproj, N * C)
+    res2, ln2 = get(a.residual2, N * C), get(a.ln2, N * C)
+    fch, fchg = get(a.fch, N * 4 * C), get(a.fch_gelu, N * 4 * C)
+    fcproj, res3 = get(a.fcproj, N * C), get(a.residual3, N * C)
+    ln1_next = get(a.ln1, N * C, N * C)
+
+    def dv(h):
+        return torch.from_numpy(np.ascontiguousarray(h, np.float32)).cuda()
+
+    def linear(inp, w, bias, cout, cin):
+        out = torch.empty(N * cout, device="cuda")
+        d_in, d_w, d_b = dv(inp), dv(w), dv(bias)
+        bmb.gemm(False, True, N, cout, cin, 1.0, d_in.data_ptr(), d_w.data_ptr(), 0.0,
+                 out.data_ptr())
+        bmb.call("bias_forward", out.data_ptr(), d_b.data_ptr(), N, cout)
+        sync("linear")
+        return out.cpu().numpy()
+
+    def layernorm(inp, w, b):
+        d_in, d_w, d_b = dv(inp), dv(w), dv(b)
+        out = torch.empty(N * C, device="cuda")
+        mean = torch.empty(N, device="cuda")
+        rstd = torch.empty(N, device="cuda")
+        bmb.call("layernorm_forward", out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                 d_in.data_ptr(), d_w.data_ptr(), d_b.data_ptr(), N, C)
+        sync("layernorm")
+        return out.cpu().numpy()
+
+    assert np.array_equal(linear(ln1, P["qkvw"][:3 * C * C], P["qkvb"][:3 * C], 3 * C, C), qkv)
+    assert np.array_equal(linear(atty, P["attprojw"][:C * C], P["attprojb"][:C], C, C), attproj)
+    assert np.array_equal(res2, get(a.encoded, N * C) + attproj)
+    assert np.array_equal(layernorm(res2, P["ln2w"][:C], P["ln2b"][:C]), ln2)
+    assert np.array_equal(linear(ln2, P["fcw"][:4 * C * C], P["fcb"][:4 * C], 4 * C, C), fch)
+    d_fch = dv(fch)
+    g_out = torch.empty(N * 4 * C, device="cuda")
+    bmb.call("gelu_forward", g_out.data_ptr(), d_fch.data_ptr(), N * 4 * C)
+    sync("gelu")
+    assert np.array_equal(g_out.cpu().numpy(), fchg)
+    assert np.array_equal(linear(fchg, P["fcprojw"][:4 * C * C], P["fcprojb"][:C], C, 4 * C), fcproj)
+    assert np.array_equal(res3, res2 + fcproj)
+    assert np.array_equal(layernorm(res3, P["ln1w"][C:2 * C], P["ln1b"][C:2 * C]), ln1_next)
