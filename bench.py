@@ -7,9 +7,12 @@ baseline: alpha=1, beta=0.5, C pre-filled; A, B, C from the reference's
 xorshift32 fill, src/bench.cu:59-66,226-228) on the headline kernel, KERNELS
 id 9 (fp32 in, fp32 products, fp32 accumulate on v_mfma_f32_32x32x2_f32).
 `value` is its GFLOP/s (2*N^3 per step, src/bench.cu:107-110). Inputs are
-resident in HBM before timing; every launch is bracketed by HIP events on
-the null stream, which is the stream the library launches on and torch's
-current stream, so `roofline.achieved` is the kernel's own average duration.
+resident in HBM before timing; W warm-up steps, then exactly K steps
+bracketed by synchronize on both sides and by a HIP event pair on the null
+stream (the stream the library launches on and torch's current stream), so
+`ms_per_step` and `roofline.achieved` come from the kernel's own average
+duration over the timed region. The flash leg times a step of forward +
+backward the same way.
 
 The same JSON line also carries (none of them is `value`):
   * config 1: N=1024, alpha=1, beta=0 for the VALU, MFMA and bf16x3 paths
@@ -82,6 +85,27 @@ def timed(fn, steps, warmup):
         b.record()
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in ev]
+
+
+def timed_steps(fn, steps, warmup):
+    """The contract's timing: `warmup` untimed steps, then exactly `steps`
+    steps bracketed by torch.cuda.synchronize() on both sides, with a HIP
+    event pair on the null stream (the stream every launch of the library
+    goes to) around the timed region. Returns (device ms per step from the
+    events, host wall-clock ms per step)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return a.elapsed_time(b) / steps, wall
 
 
 def timed_burst(fn, reps, warmup=2):
@@ -236,13 +260,14 @@ def main():
             return lambda: fn(n, n, n, alpha, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
 
         flops = 2.0 * N ** 3
-        st = stats(timed(sq(args.kernel, N), args.steps, args.warmup))
+        ms, wall = timed_steps(sq(args.kernel, N), args.steps, args.warmup)
+        st = stats(timed(sq(args.kernel, N), args.steps, 2))  # per-launch spread
         bmb.check("sgemm")
-        g = flops / st["avg_ms"] / 1e6
+        g = flops / ms / 1e6
         ent = bmb.find_kernel(args.kernel)
         bytes_alg = 4.0 * (3 * N * N + N * N)  # A, B, C read (beta != 0), C written
         line.update({
-            "value": round(g, 1), "ms_per_step": round(st["avg_ms"], 4),
+            "value": round(g, 1), "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
             "pct_of_peak": round(100 * g / 1e3 / PEAK_FP32_TFLOPS, 1),
             "config": {"workload": "sgemm M=N=K=4096 fp32 row-major alpha=1 beta=0.5, "
                                    "KERNELS id %d (%s)" % (args.kernel, ent["name"]),
@@ -252,7 +277,7 @@ def main():
                          "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(g / 1e3 / PEAK_FP32_TFLOPS, 4),
                          "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
-            "sgemm_timing_ms": {k: round(v, 4) for k, v in st.items()},
+            "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
         })
 
         if extras:
@@ -444,22 +469,28 @@ def flash_bench(args, bmb, O, torch, traffic):
     bwd = lambda: bmb.flash_backward(dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(),
                                      d_qkv.data_ptr(), out.data_ptr(), lse.data_ptr(),
                                      Bf, T, C, NH)
+    def step():
+        fwd()
+        bwd()
+
     fwd()
-    f_ms = timed(fwd, args.steps, args.warmup)
-    b_ms = timed(bwd, args.steps, args.warmup)
+    tot, wall = timed_steps(step, args.steps, args.warmup)  # one step = forward + backward
+    f_ms, _ = timed_steps(fwd, args.steps, 2)
+    b_ms, _ = timed_steps(bwd, args.steps, 2)
+    fs, bs = stats(timed(fwd, args.steps, 2)), stats(timed(bwd, args.steps, 2))
     bmb.check("flash")
     pairs = Bf * NH * T * (T + 1) / 2
     fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
-    fs, bs = stats(f_ms), stats(b_ms)
-    tot = fs["avg_ms"] + bs["avg_ms"]
     tf = (fwd_fl + bwd_fl) / tot / 1e9
     flash = {
         "metric": "flash fwd+bwd TFLOP/s @B=8,H=12,T=1024,d=64 (causal, fp32)",
-        "value": round(tf, 2), "unit": "TFLOP/s",
-        "ms_fwd": round(fs["avg_ms"], 4), "ms_bwd": round(bs["avg_ms"], 4),
-        "ms_fwd_median": round(fs["median_ms"], 4), "ms_bwd_median": round(bs["median_ms"], 4),
-        "tflops_fwd": round(fwd_fl / fs["avg_ms"] / 1e9, 2),
-        "tflops_bwd": round(bwd_fl / bs["avg_ms"] / 1e9, 2),
+        "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(tot, 4),
+        "ms_per_step_wall": round(wall, 4),
+        "ms_fwd": round(f_ms, 4), "ms_bwd": round(b_ms, 4),
+        "launch_ms_fwd_median": round(fs["median_ms"], 4),
+        "launch_ms_bwd_median": round(bs["median_ms"], 4),
+        "tflops_fwd": round(fwd_fl / f_ms / 1e9, 2),
+        "tflops_bwd": round(bwd_fl / b_ms / 1e9, 2),
         "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_TFLOPS, 1),
         "gflop_algorithmic": round((fwd_fl + bwd_fl) / 1e9, 2),
         "tflops_ref_accounting": round(4.5 * fwd_fl / tot / 1e9, 2),
