@@ -228,10 +228,16 @@ void bmb::gemm_bias_nt(int M, int N, int K, const float *A, const float *W, cons
                        float *C, float *gelu_out) {
     if (gelu_out != nullptr)
         dispatch<false, true, bmb::EPI_BIAS_GELU>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0,
-                                                  nullptr, bmb::EpiArgs{bias, gelu_out});
+                                                  nullptr, bmb::EpiArgs{bias, gelu_out, nullptr});
     else
         dispatch<false, true, bmb::EPI_BIAS>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0, nullptr,
-                                             bmb::EpiArgs{bias, nullptr});
+                                             bmb::EpiArgs{bias, nullptr, nullptr});
+}
+
+void bmb::gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B,
+                            const float *pre, float *C) {
+    dispatch<false, false, bmb::EPI_GELU_GRAD>(1, M, N, K, 1.0f, A, 0, B, 0, 0.0f, C, 0, nullptr,
+                                               bmb::EpiArgs{nullptr, nullptr, pre});
 }
 
 extern "C" {

@@ -48,26 +48,31 @@ enum Epi {
     EPI_PARTIAL = 1,    // C = acc (a split-K partial)
     EPI_BIAS = 2,       // C = acc + bias[col]
     EPI_BIAS_GELU = 3,  // C = acc + bias[col] and act = gelu(C), both stored
+    EPI_GELU_GRAD = 4,  // C = gelu'(pre) * acc, i.e. gelu_grad(pre, acc)
 };
 struct EpiArgs {
     const float *bias;  // EPI_BIAS*: N floats
     float *act;         // EPI_BIAS_GELU: M x N, same layout as C
+    const float *pre;   // EPI_GELU_GRAD: the GELU input, M x N, same layout as C
 };
 
 // The fused epilogues are the reference's separate passes in one: gemm with
 // alpha = 1, beta = 0 stores acc, bias_forward adds bias[col] (one rounding),
-// gelu_forward maps the sum (src/gpt.cu:256-277) -- the same fp32 results.
+// gelu_forward maps the sum (src/gpt.cu:256-277), gelu_backward maps the dX
+// product (src/gpt.cu:336-337) -- the same fp32 results.
 template <int EPI>
-__device__ __forceinline__ void store_out(float *C, float *act, size_t idx, float acc,
+__device__ __forceinline__ void store_out(float *C, const EpiArgs &ep, size_t idx, float acc,
                                           float alpha, float beta, float bias) {
     if (EPI == EPI_PARTIAL) {
         C[idx] = acc;
     } else if (EPI == EPI_BLAS) {
         C[idx] = epilogue(acc, alpha, beta, C + idx);
+    } else if (EPI == EPI_GELU_GRAD) {
+        C[idx] = gelu_grad(ep.pre[idx], acc);
     } else {
         const float v = acc + bias;
         C[idx] = v;
-        if (EPI == EPI_BIAS_GELU) act[idx] = gelu(v);
+        if (EPI == EPI_BIAS_GELU) ep.act[idx] = gelu(v);
     }
 }
 
@@ -304,7 +309,7 @@ struct MfmaGemm {
                 for (int r = 0; r < 16; ++r) {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (row < M)
-                        store_out<EPI>(C, ep.act, (size_t)row * N + col, acc[fi][fn][r], alpha,
+                        store_out<EPI>(C, ep, (size_t)row * N + col, acc[fi][fn][r], alpha,
                                        beta, bias);
                 }
             }
@@ -387,8 +392,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(float *C, const float *P,
     }
     for (int k = 0; k < 4; ++k) {
         if (i + k >= mn) break;
-        const float bias = EPI == EPI_BLAS ? 0.0f : ep.bias[(i + k) % N];
-        store_out<EPI>(C, ep.act, (size_t)(i + k), acc[k], alpha, beta, bias);
+        const float bias = (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) ? ep.bias[(i + k) % N] : 0.0f;
+        store_out<EPI>(C, ep, (size_t)(i + k), acc[k], alpha, beta, bias);
     }
 }
 

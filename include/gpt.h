@@ -102,7 +102,10 @@ void gpt_alloc(GPT *g);
  * 0.02/sqrt(2L), layernorm weights 1, biases 0 (src/gpt.cu:189-222). */
 void gpt_init(GPT *g, unsigned seed);
 /* src/gpt.h:73: tokens and targets are HOST arrays of B*T ids; returns the
- * mean cross-entropy loss, or 0 when targets is NULL (logits only). */
+ * mean cross-entropy loss, or 0 when targets is NULL (logits only). A token
+ * id outside [0, padded_vocab) is reported on stderr and NaN is returned
+ * with nothing launched; a target outside [0, padded_vocab) gives that
+ * position a NaN loss (nn.h). */
 float gpt_forward(GPT *g, const int *tokens, const int *targets);
 /* src/gpt.h:74: gradients of the last gpt_forward with targets, written
  * (not accumulated) into grads_mem. */
@@ -117,8 +120,9 @@ void gpt_free(GPT *g);
  * parameter order. Both return 0 on success and -1 on any I/O or format
  * error (with a message on stderr). gpt_load_checkpoint sets g->config and
  * g->T = max_seq_len from the file, then calls gpt_alloc (so set g->B and
- * g->use_flash first) and uploads the parameters; it stores up to itos_cap
- * vocabulary bytes in itos and the full count in *nvocab. */
+ * g->use_flash first, on a GPT that holds no allocation) and uploads the
+ * parameters; it stores up to itos_cap vocabulary bytes in itos and the full
+ * count in *nvocab. */
 int gpt_save_checkpoint(const GPT *g, const char *path, const char *itos, int nvocab);
 int gpt_load_checkpoint(GPT *g, const char *path, char *itos, int itos_cap, int *nvocab);
 

@@ -319,3 +319,17 @@ def test_fused_forward_matches_separate_ops(gpu):
     assert np.array_equal(linear(fchg, P["fcprojw"][:4 * C * C], P["fcprojb"][:C], C, 4 * C), fcproj)
     assert np.array_equal(res3, res2 + fcproj)
     assert np.array_equal(layernorm(res3, P["ln1w"][C:2 * C], P["ln1b"][C:2 * C]), ln1_next)
+
+
+def test_bad_token_rejected_before_launch(gpu):
+    """A token id outside [0, Vp) would index past wte on the device: gpt_forward
+    checks the host ids first, reports and returns NaN without launching."""
+    m = _model(True)
+    x, y = _batch(3)
+    ref = m.forward(x, y)
+    x_bad = x.copy()
+    x_bad[17] = CFG[2]
+    assert math.isnan(m.forward(x_bad, y))
+    x_bad[17] = -1
+    assert math.isnan(m.forward(x_bad, y))
+    assert m.forward(x, y) == ref  # the model is untouched
