@@ -45,6 +45,10 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <vector>
 
 #include "common.hpp"
@@ -155,6 +159,62 @@ struct TileT32 {
     }
 };
 
+// Global load at a uniform base plus a 32-bit byte offset: the offset stays
+// in one VGPR and the base in SGPRs (no 64-bit address arithmetic per load).
+__device__ __forceinline__ float4 ld4_at(const float *base, unsigned byte_off) {
+    return *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(base) + byte_off);
+}
+__device__ __forceinline__ float ld1_at(const float *base, unsigned byte_off) {
+    return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + byte_off);
+}
+
+// TileT32 with every load issued and no 64-bit address arithmetic: the
+// tile base is uniform (SGPRs) and each element is a 32-bit byte offset from
+// it. For a full tile the offsets are loop-invariant; a ragged tile (nrows <
+// 32, at most one per loop) re-reads row nrows-1 for the rows past the end
+// and stores zeros for them.
+template <int HS, int NT>
+struct TileT32U {
+    static constexpr int PER_T = 8 * HS / NT;
+    static_assert(PER_T >= 1 && (8 * HS) % NT == 0, "tile splits evenly over the threads");
+    float4 v[PER_T];
+    int nr;
+
+    __device__ __forceinline__ void load(const float *src, size_t rs, int nrows, int tid) {
+        nr = nrows;
+        const unsigned urs = (unsigned)rs;
+        if (nrows == 32) {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                const int e = tid + i * NT, c = e % HS, r0 = (e / HS) * 4;
+                const unsigned o = 4u * ((unsigned)r0 * urs + c);
+                v[i].x = ld1_at(src, o);
+                v[i].y = ld1_at(src, o + 4u * urs);
+                v[i].z = ld1_at(src, o + 8u * urs);
+                v[i].w = ld1_at(src, o + 12u * urs);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                const int e = tid + i * NT, c = e % HS, r0 = (e / HS) * 4;
+                v[i].x = ld1_at(src, 4u * ((unsigned)min(r0 + 0, nrows - 1) * urs + c));
+                v[i].y = ld1_at(src, 4u * ((unsigned)min(r0 + 1, nrows - 1) * urs + c));
+                v[i].z = ld1_at(src, 4u * ((unsigned)min(r0 + 2, nrows - 1) * urs + c));
+                v[i].w = ld1_at(src, 4u * ((unsigned)min(r0 + 3, nrows - 1) * urs + c));
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int ld, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, c = e % HS, r0 = (e / HS) * 4;
+            const float4 w = make_float4(r0 + 0 < nr ? v[i].x : 0.0f, r0 + 1 < nr ? v[i].y : 0.0f,
+                                         r0 + 2 < nr ? v[i].z : 0.0f, r0 + 3 < nr ? v[i].w : 0.0f);
+            bmb::st4(lds + c * ld + r0, w);
+        }
+    }
+};
+
 // Work item of workgroup `bid` among nblk tiles x BH heads.
 // longest_hi: tile nblk-1 is the longest (forward, dQ); otherwise tile 0 is
 // (dK/dV). Items are handed out longest first. With SNAKE, the k-th round of
@@ -193,20 +253,6 @@ struct Items {
     unsigned short blk[MAX_ITEMS], t0[MAX_ITEMS], t1[MAX_ITEMS];
     unsigned char split[MAX_ITEMS];
 };
-
-// Item and head of workgroup `bid`: XCD-aware as work_item, ranks taken from
-// the longest-first list.
-__device__ __forceinline__ void table_item(int bid, int BH, const Items &it, int &item,
-                                           int &bh) {
-    if (BH % NXCD == 0) {
-        const int xcd = bid % NXCD, w = bid / NXCD, hpx = BH / NXCD;
-        item = w / hpx;
-        bh = (w % hpx) * NXCD + xcd;
-    } else {
-        item = bid / BH;
-        bh = bid % BH;
-    }
-}
 
 // ------------------------------------------------------------------ forward
 
@@ -478,16 +524,18 @@ __device__ __forceinline__ void kv_tile(const float *qs, const float (&kf)[HS / 
     // dS tile for the dQ pass, row-major [query][key]: each half-wave stores
     // 32 consecutive keys of one query row per instruction.
     if (ds_out != nullptr) {
+        float *dsl = ds_out + 128 * hf + l32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ds_out[res_row(r, hf) * 32 + l32] = ds[r];
+        for (int r = 0; r < 16; ++r) dsl[(8 * (r >> 2) + (r & 3)) * 32] = ds[r];
     }
+    const float *osl = os + 4 * hf * S::LD + l32, *qsl = qs + 4 * hf * S::LD + l32;
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
-        const int qr = res_row(st, hf);
+        const int qr = 8 * (st >> 2) + (st & 3);
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-            dv[d] = mfma(p[st], os[qr * S::LD + d * 32 + l32], dv[d]);
-            dk[d] = mfma(ds[st], qs[qr * S::LD + d * 32 + l32], dk[d]);
+            dv[d] = mfma(p[st], osl[qr * S::LD + d * 32], dv[d]);
+            dk[d] = mfma(ds[st], qsl[qr * S::LD + d * 32], dk[d]);
         }
     }
 }
@@ -581,50 +629,67 @@ __device__ __forceinline__ void bwd_dq_from_ds_block(float *smem, float *__restr
     for (int d = 0; d < DT; ++d) dq[d] = zero16();
 
     // dS tiles stream from HBM with little compute per tile, so each wave
-    // keeps the next PF tiles in flight (a ring of registers).
-    constexpr int PF = 3;
-    const float *wsrow = ws + ((size_t)bh * ds_tiles_per_head(T) +
-                               (size_t)qtw * (qtw + 1) / 2 + tk0) * 1024 + l32 * 32 + 16 * hf;
+    // keeps the next PF dS tiles in flight (a ring of registers whose slot u
+    // serves tiles u, u + PF, ...; the loop is unrolled by PF so no slot is
+    // ever copied). The K tiles are prefetched PF tiles ahead too: loads
+    // complete in issue order, so a wait on a K tile loaded one tile ahead
+    // would also wait for every dS tile issued before it. Every load is
+    // issued (past its last tile a wave re-reads that tile; a wave with none
+    // reads the head's first dS tile) so the compiler's wait counts are exact.
+    constexpr int PF = 3, LDT = 36;
+    const int last = max(my_nkt - 1, 0);
+    const float *wsw = ws + ((size_t)bh * ds_tiles_per_head(T) +
+                             (my_nkt > 0 ? (size_t)qtw * (qtw + 1) / 2 + tk0 : 0)) * 1024;
+    const unsigned lane_off = 4u * (l32 * 32 + 16 * hf);
+    auto ktile = [&](int j) { return base + (size_t)(tk0 + j) * 32 * rs + C; };
+    auto krows = [&](int j) { return min(32, T - (tk0 + j) * 32); };
     float4 ring[PF][4];
+    TileT32U<HS, NT> kt[PF];
+    {
+        TileT32U<HS, NT> k0;
+        k0.load(ktile(0), rs, krows(0), tid);
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-        if (j < my_nkt) {
+        for (int j = 0; j < PF; ++j) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ring[j][i] = bmb::ld4(wsrow + (size_t)j * 1024 + 4 * i);
+            for (int i = 0; i < 4; ++i)
+                ring[j][i] = ld4_at(wsw, 4096u * min(j, last) + lane_off + 16u * i);
+            const int kj = min(j + 1, nkt - 1);
+            kt[j].load(ktile(kj), rs, krows(kj), tid);
         }
-    Tile32<HS, NT> kt;
-    kt.load(base + (size_t)tk0 * 32 * rs + C, rs, min(32, T - tk0 * 32), tid);
-    kt.store_rows(smem, S::LD, tid);
+        k0.store(smem, LDT, tid);
+    }
     __syncthreads();
 
-    for (int t = 0; t < nkt; ++t) {
-        const bool more = t + 1 < nkt;
-        const int kn = (tk0 + t + 1) * 32;  // first key of the next tile
-        if (more) kt.load(base + (size_t)kn * rs + C, rs, min(32, T - kn), tid);
-        if (t < my_nkt) {
-            const float *ks = smem + (t & 1) * S::BUF;
-            const float a[16] = {ring[0][0].x, ring[0][0].y, ring[0][0].z, ring[0][0].w,
-                                 ring[0][1].x, ring[0][1].y, ring[0][1].z, ring[0][1].w,
-                                 ring[0][2].x, ring[0][2].y, ring[0][2].z, ring[0][2].w,
-                                 ring[0][3].x, ring[0][3].y, ring[0][3].z, ring[0][3].w};
-            // Rotate the ring and start the load of tile t + PF.
+    for (int t0 = 0; t0 < nkt; t0 += PF) {
 #pragma unroll
-            for (int j = 0; j + 1 < PF; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ring[j][i] = ring[j + 1][i];
-            if (t + PF < my_nkt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    ring[PF - 1][i] = bmb::ld4(wsrow + (size_t)(t + PF) * 1024 + 4 * i);
-            }
-#pragma unroll
-            for (int st = 0; st < 16; ++st)
+        for (int u = 0; u < PF; ++u) {
+            const int t = t0 + u;
+            if (t >= nkt) break;
+            if (t < my_nkt) {
+                const float *ks = smem + (t & 1) * S::BUF + l32 * LDT + 16 * hf;
+                float4 kb[DT][4];
 #pragma unroll
                 for (int d = 0; d < DT; ++d)
-                    dq[d] = mfma(a[st], ks[(16 * hf + st) * S::LD + d * 32 + l32], dq[d]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) kb[d][i] = bmb::ld4(ks + d * 32 * LDT + 4 * i);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int d = 0; d < DT; ++d) {
+                        dq[d] = mfma(ring[u][i].x, kb[d][i].x, dq[d]);
+                        dq[d] = mfma(ring[u][i].y, kb[d][i].y, dq[d]);
+                        dq[d] = mfma(ring[u][i].z, kb[d][i].z, dq[d]);
+                        dq[d] = mfma(ring[u][i].w, kb[d][i].w, dq[d]);
+                    }
+            }
+            const unsigned tn = 4096u * min(t + PF, last);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ring[u][i] = ld4_at(wsw, tn + lane_off + 16u * i);
+            if (t + 1 < nkt) kt[u].store(smem + ((t + 1) & 1) * S::BUF, LDT, tid);
+            const int kj = min(t + 1 + PF, nkt - 1);
+            kt[u].load(ktile(kj), rs, krows(kj), tid);
+            __syncthreads();
         }
-        if (more) kt.store_rows(smem + ((t + 1) & 1) * S::BUF, S::LD, tid);
-        __syncthreads();
     }
 
     if (!active) return;
@@ -843,7 +908,8 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))
 flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
             const float *__restrict__ dout, const float *__restrict__ lse,
             const float *__restrict__ dsum, int T, int NH, int BH, float scale, float qscale,
-            float *__restrict__ ws, const Items items) {
+            float *__restrict__ ws, const Items items, const int *__restrict__ sched_off,
+            const unsigned *__restrict__ sched_ent) {
     extern __shared__ float smem[];
     constexpr int RB = 32 * WPB;
     const int nblk = (T + RB - 1) / RB;
@@ -865,16 +931,24 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
     }
     const int ntiles = (T + 31) / 32;
     int blk, bh;
-    if (MODE == 3) {
-        int it;
-        table_item(bid, BH, items, it, bh);
-        bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, items.blk[it], bh,
-                              scale, qscale, ws, items.t0[it], items.t1[it], items.split[it]);
-    } else if (MODE == 4) {
-        int it;
-        table_item(bid, BH, items, it, bh);
-        bwd_dq_from_ds_block<HS, WPB>(smem, dqkv, qkv, ws, T, NH, items.blk[it], bh, scale,
-                                      items.t0[it], items.t1[it], items.split[it]);
+    if (MODE == 3 || MODE == 4) {
+        // Persistent workgroup: the (item, head) entries the host assigned
+        // to it, one after the other.
+        const int e0 = sched_off[bid], e1 = sched_off[bid + 1];
+        for (int e = e0; e < e1; ++e) {
+            const unsigned ent = sched_ent[e];
+            const int it = (int)(ent & 0xffffu);
+            bh = (int)(ent >> 16);
+            if (e > e0) __syncthreads();  // the previous item's last LDS reads
+            if (MODE == 3)
+                bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, items.blk[it],
+                                      bh, scale, qscale, ws, items.t0[it], items.t1[it],
+                                      items.split[it]);
+            else
+                bwd_dq_from_ds_block<HS, WPB>(smem, dqkv, qkv, ws, T, NH, items.blk[it], bh,
+                                              scale, items.t0[it], items.t1[it],
+                                              items.split[it]);
+        }
     } else if (role == 0) {
         work_item<false>(bid, BH, nblk, false, 0, blk, bh);
         bwd_kv_block<HS, WPB>(smem, dqkv, qkv, dout, lse, dsum, T, NH, blk, bh, scale, qscale,
@@ -990,25 +1064,20 @@ bool fwd_hs(int cfg, float *out, float *lse, const float *qkv, int B, int T, int
 // Per-head work list of the dK/dV pass (kv = true: block = WPB*32 keys,
 // streaming query tiles from its diagonal to the end) or of the dQ-from-dS
 // pass (block = WPB*32 queries, streaming key tiles from 0 to its diagonal).
-// A block much longer than the average (> 1.5x) is split into two halves, so
-// that the longest item no longer sets the length of the whole launch; the
-// bit of a split block is set in *zero_mask. Returns false if T has more
-// blocks than the list (or the zero mask) can hold.
-bool build_items(bool kv, int T, int wpb, Items &it, unsigned long long &zero_mask) {
+// A block longer than `target` tiles is split into two halves; the bit of a
+// split block is set in *zero_mask. Returns false if T has more blocks than
+// the list (or the zero mask) can hold.
+bool build_items(bool kv, int T, int wpb, int target, Items &it, unsigned long long &zero_mask) {
     const int ntiles = (T + 31) / 32;
     const int nblk = (ntiles + wpb - 1) / wpb;
     zero_mask = 0;
     if (nblk > MAX_ITEMS) return false;
-    long long total = 0;
-    for (int k = 0; k < nblk; ++k)
-        total += kv ? ntiles - k * wpb : std::min(ntiles, (k + 1) * wpb);
     struct Item { int blk, t0, t1, split; };
     std::vector<Item> v;
     for (int k = 0; k < nblk; ++k) {
         const int t0 = kv ? k * wpb : 0, t1 = kv ? ntiles : std::min(ntiles, (k + 1) * wpb);
         const int len = t1 - t0;
-        if (nblk <= 64 && len >= 4 && 2LL * len * nblk > 3 * total &&
-            (int)v.size() + 2 <= MAX_ITEMS) {
+        if (nblk <= 64 && len > target && len >= 4 && (int)v.size() + 2 <= MAX_ITEMS) {
             const int mid = t0 + len / 2;
             v.push_back({k, t0, mid, 1});
             v.push_back({k, mid, t1, 1});
@@ -1029,45 +1098,243 @@ bool build_items(bool kv, int T, int wpb, Items &it, unsigned long long &zero_ma
     return true;
 }
 
+// Relative cost of an item: 2 per streamed tile, plus 1 for each tile that
+// holds a wave's diagonal (masked, and some waves of the workgroup idle),
+// plus 2 for a split half (its results are atomic adds).
+int item_cost(const Items &it, int i, int wpb) {
+    const int d0 = it.blk[i] * wpb, d1 = d0 + wpb;
+    const int diag = std::max(0, std::min((int)it.t1[i], d1) - std::max((int)it.t0[i], d0));
+    return 2 * (it.t1[i] - it.t0[i]) + diag + 2 * it.split[i];
+}
+
+// Longest-first placement of weighted entries onto `nbins` bins, each entry
+// going to the least loaded bin (lowest index on ties). Entries are (cost,
+// payload) and are given in the order they should be considered.
+void lpt(const std::vector<std::pair<int, unsigned>> &entries, int nbins,
+         std::vector<std::vector<std::pair<int, unsigned>>> &bins, std::vector<long long> &load) {
+    bins.assign(nbins, {});
+    load.assign(nbins, 0);
+    std::vector<std::pair<long long, int>> heap;
+    for (int b = 0; b < nbins; ++b) heap.push_back({0, b});
+    auto cmp = [](const std::pair<long long, int> &x, const std::pair<long long, int> &y) {
+        return x > y;
+    };
+    std::make_heap(heap.begin(), heap.end(), cmp);
+    for (const auto &e : entries) {
+        std::pop_heap(heap.begin(), heap.end(), cmp);
+        auto &top = heap.back();
+        bins[top.second].push_back(e);
+        top.first += e.first;
+        load[top.second] = top.first;
+        std::push_heap(heap.begin(), heap.end(), cmp);
+    }
+}
+
+// Static schedule of a backward pass over persistent workgroups, all
+// resident at once: per_cu of them on each of the ncu CUs of every XCD.
+// Workgroup g runs entries [off[g], off[g+1]) of ent, each (item index |
+// bh << 16). With B*NH a multiple of 8, workgroup g runs on XCD g % 8 (the
+// hardware hands ids round robin to the XCDs) and takes only heads bh = g
+// (mod 8), so a head's tiles are read through one L2. Within an XCD the
+// workgroups with local index w = g / 8 and w + ncu, w + 2 ncu, ... share a CU
+// (the dispatcher fills each CU once before it places a second workgroup on
+// any, as measured on MI355X), and the workgroups of a CU share its SIMDs,
+// so the run time is set by the work per CU: the (item, head) pairs are
+// placed longest first onto the least loaded CU, then each CU's pairs onto
+// its workgroups the same way. Returns the modelled run time: per CU the
+// larger of (its work / per_cu) and (its longest workgroup / 1.5), a
+// workgroup left alone on a CU running about 1.5x faster.
+double plan_schedule(const Items &it, int wpb, int BH, int ncu, int per_cu, std::vector<int> &off,
+                     std::vector<unsigned> &ent) {
+    const int nx = (BH % NXCD == 0) ? NXCD : 1;
+    if (nx == 1) ncu *= NXCD;  // one group: the CUs of all XCDs, ids still dealt round robin
+    // no more workgroups per CU than there are entries to fill them
+    const long long per_group = (long long)it.n * (BH / nx);
+    per_cu = (int)std::max(1LL, std::min<long long>(per_cu, (per_group + ncu - 1) / ncu));
+    const int wg_per_x = ncu * per_cu;
+    std::vector<std::vector<unsigned>> wg_list((size_t)wg_per_x * nx);
+    double model = 0.0;
+    for (int x = 0; x < nx; ++x) {
+        std::vector<std::pair<int, unsigned>> entries;
+        for (int i = 0; i < it.n; ++i)
+            for (int h = x; h < BH; h += nx)
+                entries.push_back({item_cost(it, i, wpb), (unsigned)i | ((unsigned)h << 16)});
+        std::stable_sort(entries.begin(), entries.end(),
+                         [](const std::pair<int, unsigned> &a, const std::pair<int, unsigned> &b) {
+                             return a.first > b.first;
+                         });
+        std::vector<std::vector<std::pair<int, unsigned>>> cu_bins, wg_bins;
+        std::vector<long long> cu_load, wg_load;
+        lpt(entries, ncu, cu_bins, cu_load);
+        for (int c = 0; c < ncu; ++c) {
+            lpt(cu_bins[c], per_cu, wg_bins, wg_load);
+            long long wmax = 0;
+            for (int k = 0; k < per_cu; ++k) {
+                wmax = std::max(wmax, wg_load[k]);
+                const int w = c + k * ncu;  // local index of the k-th workgroup on CU c
+                auto &dst = wg_list[(size_t)w * nx + x];
+                for (const auto &e : wg_bins[k]) dst.push_back(e.second);
+            }
+            model = std::max(model, std::max((double)cu_load[c] / per_cu, wmax / 1.5));
+        }
+    }
+    off.assign(1, 0);
+    ent.clear();
+    for (const auto &l : wg_list) {
+        ent.insert(ent.end(), l.begin(), l.end());
+        off.push_back((int)ent.size());
+    }
+    return model;
+}
+
+struct Sched {
+    Items items;
+    unsigned long long zero_mask = 0;
+    int wgs = 0;                  // workgroups to launch
+    int *off = nullptr;           // device, wgs + 1 entries
+    unsigned *ent = nullptr;      // device
+};
+
+// Schedules are built once per (device, pass, shape, resident workgroups) and
+// kept until the process ends.
+std::mutex g_sched_mu;
+std::map<std::tuple<int, int, int, int, int, int>, Sched> g_sched;
+
+// Work list and persistent schedule of a backward pass. The split target is
+// the one (of the block lengths minus one, or none) whose schedule has the
+// smallest modelled run time; ties keep fewer splits. per_cu = 0 (occupancy
+// unknown) gives one item per workgroup. Returns false (the caller then tries another
+// config) if BH > 65535 (the entry encoding) or the schedule cannot be
+// uploaded.
+bool get_sched(bool kv, int T, int wpb, int BH, int per_cu, Sched &out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    const auto key = std::make_tuple(dev, (int)kv, T, wpb, BH, per_cu);
+    std::lock_guard<std::mutex> lock(g_sched_mu);
+    auto found = g_sched.find(key);
+    if (found != g_sched.end()) {
+        out = found->second;
+        return true;
+    }
+    if (BH > 65535) return false;
+    // occupancy unknown: as many workgroups as (item, head) pairs
+    if (per_cu <= 0) per_cu = 1 << 20;
+    Sched s;
+    {
+        const int ntiles = (T + 31) / 32, nblk = (ntiles + wpb - 1) / wpb;
+        std::vector<int> targets = {ntiles + 1};
+        for (int k = 0; k < nblk; ++k) {
+            const int len = kv ? ntiles - k * wpb : std::min(ntiles, (k + 1) * wpb);
+            if (len >= 4) targets.push_back(len - 1);
+        }
+        std::sort(targets.begin(), targets.end(), std::greater<int>());
+        targets.erase(std::unique(targets.begin(), targets.end()), targets.end());
+        double best = -1.0;
+        std::vector<int> off, best_off;
+        std::vector<unsigned> ent, best_ent;
+        for (int target : targets) {
+            Items it;
+            unsigned long long zm = 0;
+            if (!build_items(kv, T, wpb, target, it, zm)) continue;
+            const double mk = plan_schedule(it, wpb, BH, cus_per_xcd(), per_cu, off, ent);
+            if (best < 0 || mk < best) {
+                best = mk;
+                s.items = it;
+                s.zero_mask = zm;
+                best_off.swap(off);
+                best_ent.swap(ent);
+            }
+        }
+        if (best >= 0) {
+            int *doff = nullptr;
+            unsigned *dent = nullptr;
+            const size_t nent = std::max<size_t>(1, best_ent.size());
+            if (hipMalloc(&doff, best_off.size() * sizeof(int)) == hipSuccess &&
+                hipMalloc(&dent, nent * sizeof(unsigned)) == hipSuccess &&
+                hipMemcpy(doff, best_off.data(), best_off.size() * sizeof(int),
+                          hipMemcpyHostToDevice) == hipSuccess &&
+                (best_ent.empty() ||
+                 hipMemcpy(dent, best_ent.data(), best_ent.size() * sizeof(unsigned),
+                           hipMemcpyHostToDevice) == hipSuccess)) {
+                s.wgs = (int)best_off.size() - 1;
+                s.off = doff;
+                s.ent = dent;
+            } else {
+                (void)hipGetLastError();
+                if (doff) (void)hipFree(doff);
+                if (dent) (void)hipFree(dent);
+            }
+        }
+    }
+    if (s.wgs == 0) return false;
+    g_sched[key] = s;
+    out = s;
+    return true;
+}
+
+// Workgroups of `kern` that fit on one CU at once (0 if unknown).
+template <typename K>
+int wgs_per_cu(K kern, int threads, size_t smem) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, smem) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return per_cu;
+}
+
+// Kernel of a backward launch mode, with its LDS size allowed.
+template <int HS, int WPB, int MODE, int MINW>
+auto bwd_kernel() {
+    auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
+    bmb::allow_smem(kern, BwdSmem<HS>::BYTES);
+    return kern;
+}
+
 template <int HS, int WPB, int MODE, int MINW>
 void run_bwd_mode(float *dqkv, const float *dout, const float *qkv, const float *lse,
-                  const float *dsum, int B, int T, int NH, float *ws, const Items &items) {
+                  const float *dsum, int B, int T, int NH, float *ws, const Sched &sc) {
     const int BH = B * NH;
-    const int blocks = (MODE == 3 || MODE == 4) ? BH * items.n
+    const int blocks = (MODE == 3 || MODE == 4) ? sc.wgs
                                                 : grid_blocks(BH, T, 32 * WPB) * (MODE == 0 ? 2 : 1);
     const float scale = 1.0f / sqrtf((float)HS);
-    const size_t smem = BwdSmem<HS>::BYTES;
-    auto kern = flash_bwd_k<HS, WPB, MODE, MINW>;
-    bmb::allow_smem(kern, smem);
-    bmb::launch(kern, dim3(blocks), dim3(WPB * 64), smem, nullptr, dqkv, qkv, dout, lse, dsum,
-                T, NH, BH, scale, scale * LOG2E, ws, items);
+    auto kern = bwd_kernel<HS, WPB, MODE, MINW>();
+    bmb::launch(kern, dim3(blocks), dim3(WPB * 64), BwdSmem<HS>::BYTES, nullptr, dqkv, qkv,
+                dout, lse, dsum, T, NH, BH, scale, scale * LOG2E, ws, sc.items,
+                (const int *)sc.off, (const unsigned *)sc.ent);
 }
 
 template <int HS, int WPB, int MINW>
 bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const float *qkv,
              const float *out, const float *lse, int B, int T, int NH) {
     float *ws = nullptr;
-    Items kv_it, q_it;
-    unsigned long long kv_zero = 0, q_zero = 0;
-    kv_it.n = q_it.n = 0;
+    Sched kv_sc, q_sc;
+    kv_sc.items.n = q_sc.items.n = 0;
+    const int BH = B * NH;
     if (c.ds_ws) {
-        if (!build_items(true, T, WPB, kv_it, kv_zero) || !build_items(false, T, WPB, q_it, q_zero))
+        const int threads = WPB * 64;
+        const size_t smem = BwdSmem<HS>::BYTES;
+        if (!get_sched(true, T, WPB, BH,
+                       wgs_per_cu(bwd_kernel<HS, WPB, 3, MINW>(), threads, smem), kv_sc) ||
+            !get_sched(false, T, WPB, BH,
+                       wgs_per_cu(bwd_kernel<HS, WPB, 4, MINW>(), threads, smem), q_sc))
             return false;
         ws = ds_workspace((size_t)B * NH * ds_tiles_per_head(T) * 1024 * sizeof(float));
         if (ws == nullptr) return false;  // no workspace: the caller tries another config
     }
+    const unsigned long long kv_zero = kv_sc.zero_mask, q_zero = q_sc.zero_mask;
     const long long rows = (long long)B * T * NH;
     const long long threads = rows * (HS / 4);
     bmb::launch(flash_dsum_k<HS>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                 nullptr, dsum, dout, out, T, NH, rows, dqkv, 32 * WPB, kv_zero, q_zero);
     if (c.ds_ws) {
-        run_bwd_mode<HS, WPB, 3, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, kv_it);
-        run_bwd_mode<HS, WPB, 4, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, q_it);
+        run_bwd_mode<HS, WPB, 3, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, kv_sc);
+        run_bwd_mode<HS, WPB, 4, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, ws, q_sc);
     } else if (c.fused) {
-        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
+        run_bwd_mode<HS, WPB, 0, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_sc);
     } else {
-        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
-        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_it);
+        run_bwd_mode<HS, WPB, 1, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_sc);
+        run_bwd_mode<HS, WPB, 2, MINW>(dqkv, dout, qkv, lse, dsum, B, T, NH, nullptr, kv_sc);
     }
     return true;
 }

@@ -345,7 +345,7 @@ def gpt_shapes(bmb, O, torch):
     for name, (cin, cout) in layers.items():
         x = torch.from_numpy(O.fill_normal(BT * max(cin, cout), 11)).cuda()
         w = torch.from_numpy(O.fill_normal(cout * cin, 12, 0.02)).cuda()
-        y = torch.empty(BT * max(cin, cout), device="cuda")
+        y = torch.empty(BT * max(cin, cout), device="cuda", dtype=torch.float32)
         fl = 2.0 * BT * cin * cout
         # forward y[BT,cout] = x[BT,cin] @ w[cout,cin]^T
         fwd = lambda: bmb.gemm(False, True, BT, cout, cin, 1.0, x.data_ptr(), w.data_ptr(),
@@ -460,10 +460,10 @@ def flash_bench(args, bmb, O, torch, traffic):
     dout = O.fill_normal(Bf * T * C, 0xD0D0).reshape(Bf, T, C)
     d_qkv = torch.from_numpy(qkv).cuda()
     d_dout = torch.from_numpy(dout).cuda()
-    out = torch.empty(Bf * T * C, device="cuda")
-    lse = torch.empty(Bf * NH * T, device="cuda")
-    dqkv = torch.empty(Bf * T * 3 * C, device="cuda")
-    dsum = torch.empty(Bf * NH * T, device="cuda")
+    out = torch.empty(Bf * T * C, device="cuda", dtype=torch.float32)
+    lse = torch.empty(Bf * NH * T, device="cuda", dtype=torch.float32)
+    dqkv = torch.empty(Bf * T * 3 * C, device="cuda", dtype=torch.float32)
+    dsum = torch.empty(Bf * NH * T, device="cuda", dtype=torch.float32)
     fwd = lambda: bmb.flash_forward(out.data_ptr(), lse.data_ptr(), d_qkv.data_ptr(),
                                     Bf, T, C, NH)
     bwd = lambda: bmb.flash_backward(dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(),

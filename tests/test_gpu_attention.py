@@ -82,16 +82,22 @@ def test_flash_vs_unfused(gpu, shape):
     B, T, C, NH = shape
     qkv, dout, out_u, _, _, dqkv_u = _run(B, T, C, NH, alias=True)
     d_qkv = dev(qkv)
-    out = torch.empty(B * T * C, device="cuda")
-    lse = torch.empty(B * NH * T, device="cuda")
-    dqkv = torch.empty(B * T * 3 * C, device="cuda")
-    dsum = torch.empty(B * NH * T, device="cuda")
+    out = torch.empty(B * T * C, device="cuda", dtype=torch.float32)
+    lse = torch.empty(B * NH * T, device="cuda", dtype=torch.float32)
+    dqkv = torch.empty(B * T * 3 * C, device="cuda", dtype=torch.float32)
+    dsum = torch.empty(B * NH * T, device="cuda", dtype=torch.float32)
     bmb.flash_forward(out.data_ptr(), lse.data_ptr(), d_qkv.data_ptr(), B, T, C, NH)
     d_dout = dev(dout)
     bmb.flash_backward(dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(), d_qkv.data_ptr(),
                        out.data_ptr(), lse.data_ptr(), B, T, C, NH)
     sync("flash")
-    assert O.normwise(out.cpu().numpy(), out_u)[0] < TOL
+    out_f = out.cpu().numpy()
+    # each path against the fp64 oracle first, so a failure names the path
+    ref_o, _ = O.attn_fwd_f64(qkv, B, T, C, NH)
+    e_f, e_u = O.normwise(out_f, ref_o)[0], O.normwise(out_u, ref_o)[0]
+    print("out vs oracle: flash %.2e unfused %.2e" % (e_f, e_u), flush=True)
+    assert e_f < TOL and e_u < TOL
+    assert O.normwise(out_f, out_u)[0] < TOL
     errs = _check_grads(dqkv.cpu().numpy().reshape(B, T, 3 * C),
                         dqkv_u.reshape(B, T, 3 * C).astype(np.float64), C)
     assert max(errs) < TOL, errs

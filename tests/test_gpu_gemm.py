@@ -93,7 +93,7 @@ def test_gpt_training_shapes(gpu, g):
     C0 = O.fill_normal(M * N, 0xC0C0, 1.0) if beta != 0 else None
     dA, dB = dev(A), dev(B)
     import torch
-    dC = dev(C0) if C0 is not None else torch.empty(M * N, device="cuda")
+    dC = dev(C0) if C0 is not None else torch.empty(M * N, device="cuda", dtype=torch.float32)
     print("gpt gemm %s M=%d N=%d K=%d beta=%g" % (_tag((ta, tb)), M, N, K, beta), flush=True)
     bmb.gemm(ta, tb, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
     sync("gemm")
@@ -147,9 +147,9 @@ def test_split_k(gpu, shape, trans):
     err, bad = O.normwise(outs[0], ref)
     assert bad == 0 and err < fp32_order_bound(K), err
     # operands one float off 16-byte alignment (the 32-bit load path)
-    mA = torch.zeros(A.size + 1, device="cuda")
-    mB = torch.zeros(B.size + 1, device="cuda")
-    mC = torch.zeros(C0.size + 1, device="cuda")
+    mA = torch.zeros(A.size + 1, device="cuda", dtype=torch.float32)
+    mB = torch.zeros(B.size + 1, device="cuda", dtype=torch.float32)
+    mC = torch.zeros(C0.size + 1, device="cuda", dtype=torch.float32)
     mA[1:].copy_(dA)
     mB[1:].copy_(dB)
     mC[1:].copy_(dev(C0))

@@ -288,7 +288,7 @@ def test_fused_forward_matches_separate_ops(gpu):
         return torch.from_numpy(np.ascontiguousarray(h, np.float32)).cuda()
 
     def linear(inp, w, bias, cout, cin):
-        out = torch.empty(N * cout, device="cuda")
+        out = torch.empty(N * cout, device="cuda", dtype=torch.float32)
         d_in, d_w, d_b = dv(inp), dv(w), dv(bias)
         bmb.gemm(False, True, N, cout, cin, 1.0, d_in.data_ptr(), d_w.data_ptr(), 0.0,
                  out.data_ptr())
@@ -298,9 +298,9 @@ def test_fused_forward_matches_separate_ops(gpu):
 
     def layernorm(inp, w, b):
         d_in, d_w, d_b = dv(inp), dv(w), dv(b)
-        out = torch.empty(N * C, device="cuda")
-        mean = torch.empty(N, device="cuda")
-        rstd = torch.empty(N, device="cuda")
+        out = torch.empty(N * C, device="cuda", dtype=torch.float32)
+        mean = torch.empty(N, device="cuda", dtype=torch.float32)
+        rstd = torch.empty(N, device="cuda", dtype=torch.float32)
         bmb.call("layernorm_forward", out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
                  d_in.data_ptr(), d_w.data_ptr(), d_b.data_ptr(), N, C)
         sync("layernorm")
@@ -312,7 +312,7 @@ def test_fused_forward_matches_separate_ops(gpu):
     assert np.array_equal(layernorm(res2, P["ln2w"][:C], P["ln2b"][:C]), ln2)
     assert np.array_equal(linear(ln2, P["fcw"][:4 * C * C], P["fcb"][:4 * C], 4 * C, C), fch)
     d_fch = dv(fch)
-    g_out = torch.empty(N * 4 * C, device="cuda")
+    g_out = torch.empty(N * 4 * C, device="cuda", dtype=torch.float32)
     bmb.call("gelu_forward", g_out.data_ptr(), d_fch.data_ptr(), N * 4 * C)
     sync("gelu")
     assert np.array_equal(g_out.cpu().numpy(), fchg)

@@ -25,7 +25,16 @@ import torch.nn.functional as F
 
 import oracle as O
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _float64_default():
+    """torch computes in fp64 for this module's checks; the previous default
+    comes back afterwards, so other modules' tensors keep their float32."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(prev)
 
 
 def _rng(seed):
