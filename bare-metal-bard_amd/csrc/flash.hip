@@ -29,17 +29,24 @@
 // on v_exp_f32; lse is stored in natural-log units (lse = m ln2 + ln l), the
 // quantity src/flash.cu:309 stores.
 //
-// Backward (src/flash.cu:434-466). dsum D = rowsum(dO * O), then dK/dV
-// workgroups (S = Q K^T so that P^T and dS^T are in A-operand layout for
-// dV += P^T dO, dK += dS^T Q) and dQ workgroups (S^T layout as in the
-// forward; dQ^T += K^T dS^T). dQ and dK/dV are disjoint slices of dqkv: no
-// atomics, and the result is deterministic.
+// Backward (src/flash.cu:434-466), default configs. dsum D = rowsum(dO * O);
+// then the dK/dV pass (S = Q K^T so that P^T and dS^T are in A-operand layout
+// for dV += P^T dO, dK += dS^T Q), which also stores the causal dS tiles in a
+// library-owned workspace; then the dQ pass, dQ = scale * dS K, a light
+// pass that streams those tiles. A long block may be split into two halves
+// whose results are atomic adds onto rows the dsum kernel zeroed: exactly
+// two addends onto zero, so the result does not depend on their order and
+// repeated calls give the same bits. (Configs without the workspace
+// recompute S and dP in the dQ workgroups instead.)
 //
-// Workgroup order. Work items are handed out longest first (the causal
-// triangle would otherwise leave a long tail) and, when B*NH is a multiple of
-// 8, every XCD gets a fixed set of heads: the hardware sends workgroup ids
-// x, x+8, x+16, ... to one XCD, so a head's K/V (or Q/dO) is fetched from
-// HBM into one L2 only.
+// Workgroup order. Forward: work items are handed out longest first (the
+// causal triangle would otherwise leave a long tail) in a snake order over
+// each XCD's CUs. Backward passes: persistent workgroups, as many as fit on
+// the device at once, each running a host-planned list of (block, head)
+// items placed so that every CU gets the same amount of work (see
+// plan_schedule). When B*NH is a multiple of 8, every XCD gets a fixed set of
+// heads: the hardware sends workgroup ids x, x+8, x+16, ... to one XCD, so a
+// head's K/V (or Q/dO) is fetched from HBM into one L2 only.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
