@@ -19,7 +19,11 @@
  * backward falls back to a config that recomputes S and dP instead and
  * allocates nothing; flash_attention_backward_cfg can select such a config
  * directly. Concurrent backward calls on two streams of one device share the
- * workspace and must be serialised.
+ * workspace and must be serialised. The same configs run as persistent
+ * workgroups on a per-shape work plan that the first backward call of a
+ * shape computes on the host and uploads (a few KB per pass, kept per device
+ * until the process ends): that first call therefore makes two small
+ * allocations and two synchronous copies.
  */
 #ifndef BMB_FLASH_H
 #define BMB_FLASH_H
