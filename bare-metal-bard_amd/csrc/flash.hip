@@ -222,6 +222,42 @@ struct TileT32U {
     }
 };
 
+// Tile32 with every load issued and 32-bit offsets from a uniform base, as
+// TileT32U: rows past nrows re-read row nrows-1 and are stored as zeros.
+template <int HS, int NT>
+struct Tile32U {
+    static constexpr int CPR = HS / 4;
+    static constexpr int PER_T = 32 * CPR / NT;
+    static_assert(PER_T >= 1 && (32 * CPR) % NT == 0, "tile splits evenly over the threads");
+    float4 v[PER_T];
+    int nr;
+
+    __device__ __forceinline__ void load(const float *src, size_t rs, int nrows, int tid) {
+        nr = nrows;
+        const unsigned urs = (unsigned)rs;
+        if (nrows == 32) {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
+                v[i] = ld4_at(src, 4u * ((unsigned)r * urs + c));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                const int e = tid + i * NT, r = min(e / CPR, nrows - 1), c = (e % CPR) * 4;
+                v[i] = ld4_at(src, 4u * ((unsigned)r * urs + c));
+            }
+        }
+    }
+    __device__ __forceinline__ void store_rows(float *lds, int ld, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = (e % CPR) * 4;
+            bmb::st4(lds + r * ld + c, r < nr ? v[i] : zero4());
+        }
+    }
+};
+
 // Work item of workgroup `bid` among nblk tiles x BH heads.
 // longest_hi: tile nblk-1 is the longest (forward, dQ); otherwise tile 0 is
 // (dK/dV). Items are handed out longest first. With SNAKE, the k-th round of
@@ -371,8 +407,8 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
     const int nkt = (kend + 31) / 32;
     const int my_nkt = active ? (min(T, q0w + 32) + 31) / 32 : 0;
 
-    Tile32<HS, NT> kt;
-    TileT32<HS, NT> vt;
+    Tile32U<HS, NT> kt;
+    TileT32U<HS, NT> vt;
     kt.load(base + C, rs, min(32, T), tid);
     vt.load(base + 2 * C, rs, min(32, T), tid);
     kt.store_rows(smem, S::LDK, tid);
@@ -382,10 +418,12 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
     for (int t = 0; t < nkt; ++t) {
         const int kb = t * 32;
         const bool more = t + 1 < nkt;
-        if (more) {
-            const int nr = min(32, T - kb - 32);
-            kt.load(base + (size_t)(kb + 32) * rs + C, rs, nr, tid);
-            vt.load(base + (size_t)(kb + 32) * rs + 2 * C, rs, nr, tid);
+        {
+            // next tile; the last one is loaded again at the end so that no
+            // load sits behind a branch
+            const int kn = min(kb + 32, (nkt - 1) * 32), nr = min(32, T - kn);
+            kt.load(base + (size_t)kn * rs + C, rs, nr, tid);
+            vt.load(base + (size_t)kn * rs + 2 * C, rs, nr, tid);
         }
         if (t < my_nkt) {
             const float *ks = smem + (t & 1) * S::BUF;
@@ -1363,6 +1401,8 @@ bool bwd_hs(int cfg, float *dqkv, float *dsum, const float *dout, const float *q
 // Shape legality shared by forward and backward: a supported head size.
 bool shape_ok(int B, int T, int C, int NH, int &hs) {
     if (B < 0 || T < 0 || NH <= 0 || C <= 0 || C % NH != 0) return false;
+    // Tile loads address a 32-row tile of qkv by 32-bit byte offsets.
+    if (32LL * 3 * C * (long long)sizeof(float) >= (1LL << 31)) return false;
     hs = C / NH;
     return hs == 32 || hs == 64 || hs == 128;
 }
