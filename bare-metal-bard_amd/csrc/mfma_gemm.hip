@@ -63,7 +63,7 @@ constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.894, 1},
                           {TileKind::M, 128, 128, 0.842, 2},
                           {TileKind::N, 64, 128, 0.730, 4},
                           {TileKind::S, 64, 64, 0.691, 6}};
-constexpr int SPLITS[] = {1, 2, 3, 4, 6, 8};
+constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 constexpr double K_OVERHEAD = 32.0;       // per-item prologue/epilogue, in k steps
 constexpr double HBM_BYTES_PER_S = 5e12;  // achieved, for the partials' round trip
 constexpr double LAUNCH_S = 4e-6;         // the reduce launch
