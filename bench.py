@@ -7,7 +7,10 @@ baseline: alpha=1, beta=0.5, C pre-filled; A, B, C from the reference's
 xorshift32 fill, src/bench.cu:59-66,226-228) on the headline kernel, KERNELS
 id 9 (fp32 in, fp32 products, fp32 accumulate on v_mfma_f32_32x32x2_f32).
 `value` is its GFLOP/s (2*N^3 per step, src/bench.cu:107-110). Inputs are
-resident in HBM before timing; W warm-up steps, then exactly K steps
+resident in HBM before timing; W warm-up steps (continued, untimed, until at
+least WARM_MIN_MS of warm-up work has run: the GPU's clock takes a few tens
+of milliseconds of load to settle at ~2.4 GHz, and a warm-up of a few
+milliseconds times the ramp instead), then exactly K steps
 bracketed by synchronize on both sides and by a HIP event pair on the null
 stream (the stream the library launches on and torch's current stream), so
 `ms_per_step` and `roofline.achieved` come from the kernel's own average
@@ -87,15 +90,27 @@ def timed(fn, steps, warmup):
     return [a.elapsed_time(b) for a, b in ev]
 
 
-def timed_steps(fn, steps, warmup):
-    """The contract's timing: `warmup` untimed steps, then exactly `steps`
-    steps bracketed by torch.cuda.synchronize() on both sides, with a HIP
-    event pair on the null stream (the stream every launch of the library
-    goes to) around the timed region. Returns (device ms per step from the
-    events, host wall-clock ms per step)."""
+WARM_MIN_MS = 100.0  # least warm-up work before a timed region
+WARM_STEPS_RUN = {}  # warm-up steps actually run, by region name
+
+
+def timed_steps(fn, steps, warmup, name=None):
+    """The contract's timing: `warmup` untimed steps (more, untimed, until
+    WARM_MIN_MS of warm-up has run), then exactly `steps` steps bracketed by
+    torch.cuda.synchronize() on both sides, with a HIP event pair on the null
+    stream (the stream every launch of the library goes to) around the timed
+    region. Returns (device ms per step from the events, host wall-clock ms
+    per step); the warm-up steps run are kept in WARM_STEPS_RUN[name]."""
     import torch
-    for _ in range(warmup):
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < WARM_MIN_MS:
         fn()
+        n += 1
+        if n % 8 == 0 or n >= warmup:
+            torch.cuda.synchronize()
+    if name is not None:
+        WARM_STEPS_RUN[name] = n
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -106,6 +121,102 @@ def timed_steps(fn, steps, warmup):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     return a.elapsed_time(b) / steps, wall
+
+
+class Telemetry:
+    """Clock and power of GPU 0 from amdsmi's metrics table while a `with`
+    block runs. The firmware refreshes that table about once a second, so a
+    host thread polls it and keeps each refresh (a new energy timestamp);
+    result() uses the last two refreshes that both fall inside the block:
+    average socket power = energy accumulated between them / their time
+    apart, and the per-XCD GFX clocks of the later one. A block shorter than
+    about two refreshes has no such pair, and says so."""
+
+    def __init__(self, period=0.02):
+        self.period, self.snaps, self.reason = period, [], None
+        self.smi = self.h = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            hs = amdsmi.amdsmi_get_processor_handles()
+            if not hs:
+                raise RuntimeError("no GPU handle")
+            self.smi, self.h = amdsmi, hs[0]
+        except Exception as e:  # not fatal: the figures are reported without it
+            self.reason = "amdsmi unavailable: %s" % (repr(e)[:120],)
+
+    def _snap(self):
+        smi = self.smi
+        e = smi.amdsmi_get_energy_count(self.h)
+        m = smi.amdsmi_get_gpu_metrics_info(self.h)
+        clks = m.get("current_gfxclks")
+        if not isinstance(clks, (list, tuple)):
+            clks = [m.get("current_gfxclk")]
+        clks = [int(c) for c in clks if isinstance(c, (int, float)) and c < 0xFFFF]
+        return (int(e["timestamp"]), int(e["energy_accumulator"]),
+                float(e["counter_resolution"]), clks)
+
+    def __enter__(self):
+        import threading
+        self.snaps, self._stop = [], threading.Event()
+        if self.h is not None:
+            try:
+                self._first_ts = self._snap()[0]  # the refresh current at entry
+            except Exception as e:
+                self.reason = "amdsmi query failed: %s" % (repr(e)[:120],)
+                self.h = None
+        if self.h is not None:
+            def run():
+                last = self._first_ts
+                while not self._stop.is_set():
+                    try:
+                        sn = self._snap()
+                    except Exception as e:
+                        self.reason = "amdsmi query failed: %s" % (repr(e)[:120],)
+                        return
+                    if sn[0] != last:
+                        self.snaps.append(sn)
+                        last = sn[0]
+                    self._stop.wait(self.period)
+            self._thr = threading.Thread(target=run, daemon=True)
+            self._thr.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self.h is not None:
+            self._thr.join()
+        return False
+
+    def result(self):
+        # The first refresh seen inside the block still averages time before
+        # it; a pair of later refreshes covers an interval inside the block.
+        if len(self.snaps) < 3:
+            return {"available": False,
+                    "reason": self.reason or "region shorter than two refreshes (~1 s each) "
+                                             "of amdsmi's metrics table"}
+        (t0, e0, res, _), (t1, e1, _, clks) = self.snaps[-2], self.snaps[-1]
+        dt = (t1 - t0) / 1e9  # ns
+        clk = sorted(clks)
+        return {"socket_power_w": round((e1 - e0) * res * 1e-6 / dt, 1), "window_s": round(dt, 3),
+                "gfx_clk_mhz_per_xcd": clks,
+                "gfx_clk_mhz_median": clk[len(clk) // 2] if clk else None,
+                "gfx_clk_mhz_max_spec": 2400}
+
+
+def sustained_telemetry(fn, seconds=3.5):
+    """Clock and power under `fn` run back to back for `seconds` (untimed, after
+    the timed region): long enough for two refreshes of amdsmi's metrics."""
+    import torch
+    with Telemetry() as tel:
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+    return tel.result()
 
 
 def timed_burst(fn, reps, warmup=2):
@@ -260,7 +371,7 @@ def main():
             return lambda: fn(n, n, n, alpha, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
 
         flops = 2.0 * N ** 3
-        ms, wall = timed_steps(sq(args.kernel, N), args.steps, args.warmup)
+        ms, wall = timed_steps(sq(args.kernel, N), args.steps, args.warmup, "sgemm")
         st = stats(timed(sq(args.kernel, N), args.steps, 2))  # per-launch spread
         bmb.check("sgemm")
         g = flops / ms / 1e6
@@ -278,6 +389,8 @@ def main():
                          "frac": round(g / 1e3 / PEAK_FP32_TFLOPS, 4),
                          "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
             "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
+            "warmup_steps_run": WARM_STEPS_RUN.get("sgemm"),
+            "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
         })
 
         if extras:
@@ -413,6 +526,15 @@ def gpt_step_bench(args, bmb, torch):
         losses.append(loss)
         norms.append(gn)
     bmb.check("gpt step")
+
+    def more_steps():  # untimed training steps for the clock / power reading
+        x, y = batches[0]
+        m.forward(x, y)
+        m.backward()
+        g = L.grad_global_norm(m.g.grads_mem, n_params)
+        L.adamw_update(m.g.params_mem, m.g.grads_mem, m.g.m_mem, m.g.v_mem, n_params, 1e-4,
+                       0.9, 0.999, 1e-8, 0.1, total + 1, 1.0 / g if g > 1.0 else 1.0)
+    tel = sustained_telemetry(more_steps)
     # one more step split into its phases, for the breakdown
     x, y = batches[0]
     torch.cuda.synchronize()
@@ -446,6 +568,7 @@ def gpt_step_bench(args, bmb, torch):
         "loss_first": round(losses[0], 5), "loss_last": round(losses[-1], 5),
         "ln_V": round(float(np.log(cfg[1])), 5),
         "grad_norm_first": round(norms[0], 5),
+        "device_telemetry_sustained": tel,
         "config": {"workload": "GPT-2 small train step: 12L/768/12H, T=1024, B=8, V=50257 "
                                "(Vp=50304), fused attention, grad clip 1.0, AdamW "
                                "(0.9, 0.999, 1e-8, wd 0.1), lr schedule of train_gpt.cu",
@@ -474,7 +597,7 @@ def flash_bench(args, bmb, O, torch, traffic):
         bwd()
 
     fwd()
-    tot, wall = timed_steps(step, args.steps, args.warmup)  # one step = forward + backward
+    tot, wall = timed_steps(step, args.steps, args.warmup, "flash")  # one step = fwd + bwd
     f_ms, _ = timed_steps(fwd, args.steps, 2)
     b_ms, _ = timed_steps(bwd, args.steps, 2)
     fs, bs = stats(timed(fwd, args.steps, 2)), stats(timed(bwd, args.steps, 2))
@@ -496,6 +619,8 @@ def flash_bench(args, bmb, O, torch, traffic):
         "tflops_ref_accounting": round(4.5 * fwd_fl / tot / 1e9, 2),
         "fwd_config": bmb.flash_configs()[bmb.flash_default_config()],
         "bwd_config": bmb.flash_bwd_configs()[bmb.flash_default_bwd_config()],
+        "warmup_steps_run": WARM_STEPS_RUN.get("flash"),
+        "device_telemetry_sustained": sustained_telemetry(step),
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
                      "traffic": traffic.get("flash_fwd_bwd_b8h12t1024d64")},
