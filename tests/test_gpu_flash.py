@@ -175,6 +175,29 @@ def test_backward_deterministic(gpu, shape):
     assert np.array_equal(first.view(np.uint32), second.view(np.uint32))
 
 
+def test_many_heads_fall_back(gpu):
+    """B*NH above 65535 does not fit the persistent backward's work-list
+    encoding: the default config declines (nothing launched) and the
+    wrapper runs a recompute config instead. The first batches are checked
+    against the oracle (it works per (b, h))."""
+    B, T, C, NH = 65537, 3, 32, 1
+    qkv = O.fill_xorshift(B * T * 3 * C, 4321).reshape(B, T, 3 * C)
+    dout = O.fill_xorshift(B * T * C, 8765).reshape(B, T, C)
+    d_qkv, out, lse = _run_fwd(qkv, B, T, C, NH)
+    import torch
+    x = torch.empty(B * T * 3 * C, device="cuda", dtype=torch.float32)
+    assert not bmb.flash_backward_cfg(bmb.flash_default_bwd_config(), x.data_ptr(), x.data_ptr(),
+                                      dev(dout).data_ptr(), d_qkv.data_ptr(), out.ptr, lse.ptr,
+                                      B, T, C, NH)
+    dq, _ = _run_bwd(d_qkv, out, lse, dout, B, T, C, NH)
+    nb = 4
+    ref_o, _ = O.attn_fwd_f64(qkv[:nb], nb, T, C, NH)
+    assert O.normwise(out.get().reshape(B, T, C)[:nb], ref_o)[0] < TOL
+    ref_d = O.attn_bwd_f64(qkv[:nb], dout[:nb], nb, T, C, NH)
+    for e in _check_grads(dq[:nb], ref_d, C):
+        assert e < TOL
+
+
 def test_bad_head_size_rejected(gpu):
     """_cfg returns false and launches nothing for hs outside {32, 64, 128}."""
     import torch
