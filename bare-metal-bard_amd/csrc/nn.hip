@@ -391,23 +391,27 @@ __global__ __launch_bounds__(NT) void colsum_k(float *partial, const float *dout
 }
 
 // dst0[c] += sum_g partial[g][c] for c < C0, dst1[c - C0] += ... for the rest
-// (width columns in all). A workgroup covers 32 columns with 8 slices of
-// lanes: slice q sums g = q, q+8, ... in order, then the 8 slice sums are
-// added in slice order.
+// (width columns in all). A workgroup covers FIN_COLS columns with
+// NT / FIN_COLS slices of lanes: slice q sums g = q, q + slices, ... in order,
+// then the slice sums are added in slice order. Few columns per workgroup
+// and many slices keep each lane's chain of dependent adds short (the
+// partials are a few hundred rows and sit in L2; this kernel is latency-
+// bound, not bandwidth-bound).
+constexpr int FIN_COLS = 8;
 __global__ __launch_bounds__(NT) void colsum_finish_k(float *dst0, float *dst1, int C0,
                                                        const float *partial, int G, int width) {
-    __shared__ float sl[8][32];
-    const int col = threadIdx.x & 31, q = threadIdx.x >> 5;
-    const int c = blockIdx.x * 32 + col;
+    constexpr int SL = NT / FIN_COLS;
+    __shared__ float sl[SL][FIN_COLS];
+    const int col = threadIdx.x % FIN_COLS, q = threadIdx.x / FIN_COLS;
+    const int c = blockIdx.x * FIN_COLS + col;
     float s = 0.0f;
     if (c < width)
-        for (int g = q; g < G; g += 8) s += partial[(size_t)g * width + c];
+        for (int g = q; g < G; g += SL) s += partial[(size_t)g * width + c];
     sl[q][col] = s;
     __syncthreads();
     if (q == 0 && c < width) {
         float t = sl[0][col];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) t += sl[k][col];
+        for (int k = 1; k < SL; ++k) t += sl[k][col];
         if (c < C0)
             dst0[c] += t;
         else
@@ -756,8 +760,8 @@ void colsum_shape(int N, int C, int &rpc, int &G) {
 }
 
 void colsum_finish(float *d0, float *d1, int C0, const float *partial, int G, int width) {
-    bmb::launch(colsum_finish_k, dim3(ceil_div(width, 32)), dim3(NT), 0, nullptr, d0, d1, C0,
-                partial, G, width);
+    bmb::launch(colsum_finish_k, dim3(ceil_div(width, FIN_COLS)), dim3(NT), 0, nullptr, d0, d1,
+                C0, partial, G, width);
 }
 
 template <int NCH, bool RES = false>

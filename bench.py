@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--kernel", type=int, default=9, help="headline KERNELS id")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-telemetry", action="store_true",
+                    help="skip the untimed sustained runs that read clock and power (for "
+                         "profiling runs, whose per-step kernel totals they would inflate)")
     ap.add_argument("--no-ladder", action="store_true", help="skip the ladder, sweep and GPT shapes")
     ap.add_argument("--quick", action="store_true", help="headline SGEMM and flash only")
     ap.add_argument("--only", choices=["sgemm", "flash", "gpt"], default=None,
@@ -204,10 +207,15 @@ class Telemetry:
                 "gfx_clk_mhz_max_spec": 2400}
 
 
+SKIP_TELEMETRY = False  # --no-telemetry
+
+
 def sustained_telemetry(fn, seconds=3.5):
     """Clock and power under `fn` run back to back for `seconds` (untimed, after
     the timed region): long enough for two refreshes of amdsmi's metrics."""
     import torch
+    if SKIP_TELEMETRY:
+        return {"available": False, "reason": "--no-telemetry"}
     with Telemetry() as tel:
         t0, n = time.perf_counter(), 0
         while time.perf_counter() - t0 < seconds:
@@ -319,7 +327,9 @@ def gf(flops, ms):
 
 
 def main():
+    global SKIP_TELEMETRY
     args = parse()
+    SKIP_TELEMETRY = args.no_telemetry
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU tier); "
               "--gpus %d is not supported" % args.gpus, file=sys.stderr)
