@@ -21,7 +21,7 @@
 namespace {
 
 using bmb::MfmaTile;
-using TileL = MfmaTile<256, 256, 16, 2, 4>;  // 512 lanes, 128x64 per wave
+using TileL = MfmaTile<256, 256, 32, 2, 4>;  // 512 lanes, 128x64 per wave, K depth 32
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
 using TileN = MfmaTile<64, 128, 16, 2, 2>;   // 256 lanes, 32x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
@@ -59,7 +59,7 @@ struct Cand {
     double eff;
     int occ;
 };
-constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.894, 1},
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.912, 1},
                           {TileKind::M, 128, 128, 0.842, 2},
                           {TileKind::N, 64, 128, 0.730, 4},
                           {TileKind::S, 64, 64, 0.691, 6}};
@@ -78,6 +78,7 @@ struct Plan {
 };
 
 inline int round_up16(long long x) { return (int)((x + 15) / 16 * 16); }
+inline int round_up32(long long x) { return (int)((x + 31) / 32 * 32); }
 
 double model_time(long long M, long long N, long long K, long long batch, const Cand &c,
                   int splits, int kchunk, int cus) {
@@ -111,7 +112,7 @@ Plan pick(int M, int N, int K, int batch, bool may_split) {
             int splits = 1, kchunk = round_up16(K);
             if (s > 1) {
                 if (!may_split || K < 2 * MIN_SPLIT_K) continue;
-                kchunk = round_up16((K + s - 1) / s);
+                kchunk = round_up32((K + s - 1) / s);  // whole k-tiles of every tile's BK
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
                 if (splits < 2 || (long long)splits * M * N > MAX_SPLIT_FLOATS) continue;

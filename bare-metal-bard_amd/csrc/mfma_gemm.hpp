@@ -333,7 +333,8 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
 }
 
 // Split-K: blockIdx.y = split s covers k in [s*kchunk, min(K, (s+1)*kchunk))
-// (kchunk a multiple of BK) and writes its raw fp32 sums to the M x N
+// (kchunk a multiple of 16; the host rounds it to a multiple of 32, whole
+// k-tiles of every tile it uses) and writes its raw fp32 sums to the M x N
 // partial P + s*M*N; splitk_reduce_k then adds the splits in order.
 template <bool TA, bool TB, class Tile, bool VEC>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
