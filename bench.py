@@ -400,6 +400,7 @@ def main():
                          "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
             "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
             "warmup_steps_run": WARM_STEPS_RUN.get("sgemm"),
+            "vendor_fp32_gemm_gflops": vendor_sq(torch, dA, dB, dC, N),
             "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
         })
 
@@ -457,11 +458,25 @@ def main():
     print(json.dumps(line))
 
 
+def vendor_sq(torch, dA, dB, dC, N):
+    """Context only, not this build's result: the vendor's fp32 GEMM (hipBLASLt
+    through torch, TF32 off) on the headline problem, C = A@B + 0.5*C, timed
+    like the headline (warm-up, then a burst of 20)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    A = dA[:N * N].view(N, N)
+    B = dB[:N * N].view(N, N)
+    Cm = dC[:N * N].view(N, N)
+    fn = lambda: Cm.addmm_(A, B, beta=0.5)
+    timed_steps(fn, 5, 5)
+    return gf(2.0 * N ** 3, timed_burst(fn, 20))
+
+
 def gpt_shapes(bmb, O, torch):
     """gemm() at the GPT-2-small training shapes (src/gpt.cu:256-376): the
     forward is NT (weights stored out x in), the backward dX is NN with
     beta 0 and dW is TN with beta 1 (accumulate)."""
     BT, C, V = GPT["BT"], GPT["C"], GPT["V"]
+    torch.backends.cuda.matmul.allow_tf32 = False  # the vendor comparison stays fp32
     layers = {"qkv": (C, 3 * C), "attn_proj": (C, C), "mlp_fc": (C, 4 * C),
               "mlp_proj": (4 * C, C), "lm_head": (C, V)}
     res = {}
@@ -485,6 +500,15 @@ def gpt_shapes(bmb, O, torch):
                      "dX_NN": gf(fl, timed_burst(dxf, reps)),
                      "dW_TN_beta1": gf(fl, timed_burst(dwf, reps))}
         bmb.check("gemm " + name)
+        # Context only, not this build's result: the vendor's fp32 GEMM
+        # (hipBLASLt through torch, TF32 off) on the same operands.
+        X, Y = x[:BT * cin].view(BT, cin), y[:BT * cout].view(BT, cout)
+        W = w.view(cout, cin)
+        Yo, Xo = y[:BT * cout].view(BT, cout), x[:BT * cin].view(BT, cin)
+        res[name]["vendor_fp32"] = {
+            "fwd_NT": gf(fl, timed_burst(lambda: torch.matmul(X, W.t(), out=Yo), reps)),
+            "dX_NN": gf(fl, timed_burst(lambda: torch.matmul(Yo, W, out=Xo), reps)),
+            "dW_TN_beta1": gf(fl, timed_burst(lambda: W.addmm_(Yo.t(), Xo), reps))}
         del x, w, y
     torch.cuda.empty_cache()
     return res
