@@ -281,14 +281,18 @@ struct MfmaGemm {
                     } else {
                         // Publish the next stage, start the global loads of
                         // the one after, and read group 0 of the next stage
-                        // while this tile's last MFMAs run.
+                        // while this tile's last MFMAs run. Unconditional on
+                        // purpose: past the last tile the loads are zero fills
+                        // (k >= K, no memory access), the store and the reads
+                        // touch the idle LDS stage, and their results are never
+                        // used. Guarding them makes the compiler copy the
+                        // fragment registers and wait for the reads before
+                        // this group's MFMAs.
                         float *nxt = smem + ((kt + 1) & 1) * L::STAGE;
-                        if (kt + 1 < nkt) store(g, nxt, nxt + L::A_SZ, tid);
-                        if (kt + 2 < nkt)
-                            load(g, A, B, M, N, K, lda, ldb, m0, n0, (kt + 2) * BK, tid);
+                        store(g, nxt, nxt + L::A_SZ, tid);
+                        load(g, A, B, M, N, K, lda, ldb, m0, n0, (kt + 2) * BK, tid);
                         __syncthreads();
-                        if (kt + 1 < nkt)
-                            fragments(nxt, nxt + L::A_SZ, 0, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
+                        fragments(nxt, nxt + L::A_SZ, 0, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
                     }
                     mma(fa[cb], fb[cb], acc);
                 }
