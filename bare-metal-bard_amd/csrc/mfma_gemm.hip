@@ -21,10 +21,7 @@
 namespace {
 
 using bmb::MfmaTile;
-// 512 lanes, 128x64 per wave. K depth 16 for NN, 32 otherwise: measured at
-// N = 4096 / 8192, NN runs ~1% faster at 16, TN and NT 1-2% faster at 32.
-template <bool TA, bool TB>
-using TileL = MfmaTile<256, 256, (!TA && !TB) ? 16 : 32, 2, 4>;
+using TileL = MfmaTile<256, 256, 32, 2, 4>;  // 512 lanes, 128x64 per wave, K depth 32
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
 using TileN = MfmaTile<64, 128, 16, 2, 2>;   // 256 lanes, 32x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
@@ -62,10 +59,10 @@ struct Cand {
     double eff;
     int occ;
 };
-constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.912, 1},
-                          {TileKind::M, 128, 128, 0.842, 2},
-                          {TileKind::N, 64, 128, 0.730, 4},
-                          {TileKind::S, 64, 64, 0.691, 6}};
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.976, 1},
+                          {TileKind::M, 128, 128, 0.946, 2},
+                          {TileKind::N, 64, 128, 0.752, 4},
+                          {TileKind::S, 64, 64, 0.712, 6}};
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 constexpr double K_OVERHEAD = 32.0;       // per-item prologue/epilogue, in k steps
 constexpr double HBM_BYTES_PER_S = 5e12;  // achieved, for the partials' round trip
@@ -194,7 +191,7 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     }
     if (p.splits > 1) {
         switch (p.tile.kind) {
-        case TileKind::L: launch_split<TA, TB, TileL<TA, TB>, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
+        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
         case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
         case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
         case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
@@ -203,7 +200,7 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     }
     switch (p.tile.kind) {
     case TileKind::L:
-        launch_tile<TA, TB, TileL<TA, TB>, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
+        launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     case TileKind::M:
         launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);

@@ -231,10 +231,18 @@ def timed_burst(fn, reps, warmup=2):
     """Average duration (ms) of `reps` back-to-back launches between one pair
     of HIP events: the throughput of a kernel in a stream, as the training
     step runs it. Per-launch event pairs add a gap of tens of microseconds
-    around each launch, which distorts kernels of a few hundred microseconds."""
+    around each launch, which distorts kernels of a few hundred microseconds.
+    Like timed_steps, the warm-up runs at least WARM_MIN_MS of the workload:
+    after a switch of workload the clock takes tens of ms to settle (a
+    2-launch warm-up put N=4096 SGEMM 7% below its settled rate)."""
     import torch
-    for _ in range(warmup):
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < WARM_MIN_MS:
         fn()
+        n += 1
+        if n % 8 == 0 or n >= warmup:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
