@@ -42,16 +42,20 @@ int device_cus() {
 }
 
 // Tile and split-K choice from a time model fitted to MI355X measurements of
-// every tile and split on the GPT-2 training shapes and the square sweep
-// 512 ... 8192 (both transposes). Per tile: `eff`, the fraction of the fp32
-// MFMA peak a CU reaches when it is full of such workgroups, and `occ`, the
-// workgroups that share a CU. A work item is one output tile over one K
-// split; the machine runs cus * occ of them per round, so an item count just
-// above a whole number of rounds costs a nearly empty extra round (4097^3 on
-// 256x256: 289 tiles on 256 CUs). Splitting K multiplies the items of a
-// problem with few output tiles (768 x 768 x 8192 has 144 on 64x64) and costs
-// the partials' round trip through HBM plus one reduce launch. The model only
-// compares candidates; its times are not predictions.
+// every tile and split on the GPT-2 training shapes and a square sweep 512 ...
+// 8192 (both transposes; 32 shapes, about 1500 timed plans): the fit picks
+// the measured best plan on 27 of them and is within 3% on all but N = 1000.
+// Per tile: `eff`, the fraction of the fp32 MFMA peak a CU reaches when it is
+// full of such workgroups, and `occ`, the workgroups that share a CU. A work
+// item is one output tile over one K split; the machine runs cus * occ of
+// them per round, so an item count just above a whole number of rounds costs
+// an extra round (4097^3 on 256x256: 289 tiles on 256 CUs); a last round in
+// which each CU holds fewer than occ items runs faster per item, by
+// (held / occ)^PARTIAL_EXP. Splitting K multiplies the items of a problem with
+// few output tiles (768 x 768 x 8192 has 144 on 64x64) and costs the
+// partials' round trip (mostly through the 256 MB last-level cache, hence a
+// rate above HBM's) plus one reduce launch. The model only compares
+// candidates; its times are not predictions.
 enum class TileKind { L, M, N, S };
 struct Cand {
     TileKind kind;
@@ -59,15 +63,16 @@ struct Cand {
     double eff;
     int occ;
 };
-constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.976, 1},
-                          {TileKind::M, 128, 128, 0.946, 2},
-                          {TileKind::N, 64, 128, 0.752, 4},
-                          {TileKind::S, 64, 64, 0.712, 6}};
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.89, 1},
+                          {TileKind::M, 128, 128, 0.88, 2},
+                          {TileKind::N, 64, 128, 0.80, 4},
+                          {TileKind::S, 64, 64, 0.80, 6}};
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
-constexpr double K_OVERHEAD = 32.0;       // per-item prologue/epilogue, in k steps
-constexpr double HBM_BYTES_PER_S = 5e12;  // achieved, for the partials' round trip
-constexpr double LAUNCH_S = 4e-6;         // the reduce launch
-constexpr int MIN_SPLIT_K = 128;          // shortest K range a split may get
+constexpr double K_OVERHEAD = 72.0;           // per-item prologue/epilogue, in k steps
+constexpr double PARTIAL_EXP = 0.89;          // speed of a part-filled last round
+constexpr double PARTIALS_BYTES_PER_S = 1.8e13;  // the partials' round trip
+constexpr double LAUNCH_S = 1.4e-6;           // the reduce launch
+constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
 // Largest split-K partial buffer (floats): 256 MiB per host thread and device.
 constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;
 
@@ -90,13 +95,11 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     const long long full = items / slots, rem = items % slots;
     double t = full * t_item;
     if (rem) {
-        // A partial round: CUs holding fewer than occ items run each faster,
-        // but one item alone does not get the whole CU.
+        // A partial round: CUs holding fewer than occ items run each faster.
         const long long per_cu = (rem + cus - 1) / cus;
-        t += per_cu < c.occ ? t_item * std::max<long long>(per_cu, std::min(c.occ, 2)) / c.occ
-                            : t_item;
+        t += per_cu < c.occ ? t_item * pow((double)per_cu / c.occ, PARTIAL_EXP) : t_item;
     }
-    if (splits > 1) t += (splits + 2.0) * M * N * 4.0 / HBM_BYTES_PER_S + LAUNCH_S;
+    if (splits > 1) t += (splits + 2.0) * M * N * 4.0 / PARTIALS_BYTES_PER_S + LAUNCH_S;
     return t;
 }
 
