@@ -373,10 +373,30 @@ struct MfmaGemm {
         }
 
         // Epilogue: lanes 0-31 of a register cover 32 consecutive columns, so
-        // each C row segment is one 128-byte coalesced access.
+        // each C row segment is one 128-byte coalesced access. What an
+        // epilogue reads (C when beta != 0, the GELU input) is gathered for a
+        // row of FN blocks before any of their results is stored, so 16 * FN
+        // loads per lane are in flight at once; read-use-store per element
+        // would cost one memory round trip per output. Same arithmetic as
+        // store_out.
         const int l32 = lane & 31, half = lane >> 5;
+        const bool reads = EPI == EPI_GELU_GRAD || (EPI == EPI_BLAS && beta != 0.0f);
+        const float *src = EPI == EPI_GELU_GRAD ? ep.pre : C;
 #pragma unroll
-        for (int fi = 0; fi < FM; ++fi)
+        for (int fi = 0; fi < FM; ++fi) {
+            float in[FN][16];
+            if (reads) {
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    const int col = n0 + wn + fn * 32 + l32;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                        in[fn][r] = (INTERIOR || (row < M && col < N))
+                                        ? src[(size_t)row * N + col] : 0.0f;
+                    }
+                }
+            }
 #pragma unroll
             for (int fn = 0; fn < FN; ++fn) {
                 const int col = n0 + wn + fn * 32 + l32;
@@ -385,11 +405,24 @@ struct MfmaGemm {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (INTERIOR || row < M)
-                        store_out<EPI>(C, ep, (size_t)row * N + col, acc[fi][fn][r], alpha,
-                                       beta, bias);
+                    if (!INTERIOR && row >= M) continue;
+                    const size_t idx = (size_t)row * N + col;
+                    const float a = acc[fi][fn][r];
+                    float v;
+                    if (EPI == EPI_PARTIAL) {
+                        v = a;
+                    } else if (EPI == EPI_BLAS) {
+                        v = reads ? fma_rn(alpha, a, beta * in[fn][r]) : alpha * a;
+                    } else if (EPI == EPI_GELU_GRAD) {
+                        v = gelu_grad(in[fn][r], a);
+                    } else {
+                        v = a + bias;
+                        if (EPI == EPI_BIAS_GELU) ep.act[idx] = gelu(v);
+                    }
+                    C[idx] = v;
                 }
             }
+        }
     }
 
     // Picks the interior path when it applies (a uniform branch per workgroup).
