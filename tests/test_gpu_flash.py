@@ -186,8 +186,9 @@ def test_many_heads_fall_back(gpu):
     d_qkv, out, lse = _run_fwd(qkv, B, T, C, NH)
     import torch
     x = torch.empty(B * T * 3 * C, device="cuda", dtype=torch.float32)
+    d_dout = dev(dout)
     assert not bmb.flash_backward_cfg(bmb.flash_default_bwd_config(), x.data_ptr(), x.data_ptr(),
-                                      dev(dout).data_ptr(), d_qkv.data_ptr(), out.ptr, lse.ptr,
+                                      d_dout.data_ptr(), d_qkv.data_ptr(), out.ptr, lse.ptr,
                                       B, T, C, NH)
     dq, _ = _run_bwd(d_qkv, out, lse, dout, B, T, C, NH)
     nb = 4

@@ -49,6 +49,35 @@ def test_gemm_shapes(gpu, shape, trans):
     assert err < fp32_order_bound(K)  # fp32 products; only the summation order differs
 
 
+# Tiles that lie wholly inside C with K one to four k-tiles deep: the
+# interior path's unguarded loads and its prefetch index, clamped to the last
+# k-tile, on every tile size the planner can pick (4096^2 takes 256x256).
+# Small-integer entries (|a|, |b| <= 8, K <= 64) make every fp32 sum exact,
+# so the result must equal the exact product bit for bit.
+SHORT_K = [(1024, 1024, 16), (512, 768, 32), (2048, 256, 48), (256, 256, 32),
+           (4096, 4096, 32), (768, 192, 64)]
+
+
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("shape", SHORT_K, ids=lambda s: "%dx%dx%d" % s)
+def test_interior_short_k_exact(gpu, shape, trans):
+    M, N, K = shape
+    ta, tb = trans
+    r = np.random.default_rng(M + 7 * N + 31 * K)
+    A = r.integers(-8, 9, M * K).astype(np.float32)
+    B = r.integers(-8, 9, K * N).astype(np.float32)
+    print("gemm exact %s M=%d N=%d K=%d" % (_tag(trans), M, N, K), flush=True)
+    dA, dB = dev(A), dev(B)  # kept alive until the launch has run
+    gC = Guarded(M * N, fill=np.full(M * N, np.nan, np.float32))
+    bmb.gemm(ta, tb, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.0, gC.ptr)
+    sync("gemm exact")
+    assert gC.ok()
+    Am = A.reshape(K, M).T if ta else A.reshape(M, K)
+    Bm = B.reshape(N, K).T if tb else B.reshape(K, N)
+    ref = (Am.astype(np.float64) @ Bm.astype(np.float64)).astype(np.float32).reshape(-1)
+    assert np.array_equal(gC.get(), ref)
+
+
 BSHAPES = [(96, 256, 256, 64), (96, 256, 64, 256), (24, 64, 64, 32), (8, 100, 48, 33)]
 
 
