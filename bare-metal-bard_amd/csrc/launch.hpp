@@ -5,24 +5,28 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <set>
+#include <utility>
 
 #include "status.hpp"
 
 namespace bmb {
 
 // Kernels whose dynamic LDS exceeds the 64 KiB default get their limit raised
-// once per device (gfx950 has 160 KiB per CU).
+// once per kernel and device (gfx950 has 160 KiB per CU). Keyed on the
+// kernel's address: kernels of one signature share this instantiation.
 template <typename K>
 inline void allow_smem(K kern, size_t bytes) {
     if (bytes <= 65536) return;
-    static std::once_flag once[64];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
-    std::call_once(once[dev], [&] {
-        note_launch_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)bytes));
-    });
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    const void *f = reinterpret_cast<const void *>(kern);
+    static std::mutex mu;
+    static std::set<std::pair<int, const void *>> done;
+    std::lock_guard<std::mutex> lock(mu);  // held until the attribute is set
+    if (!done.insert({dev, f}).second) return;
+    note_launch_status(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)bytes));
 }
 
 template <typename... KArgs, typename... Args>

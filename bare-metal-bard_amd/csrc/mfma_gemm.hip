@@ -10,6 +10,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
@@ -44,37 +45,61 @@ int device_cus() {
 // Tile and split-K choice from a time model fitted to MI355X measurements of
 // every tile and split on the GPT-2 training shapes and a square sweep 512 ...
 // 8192 (both transposes; 32 shapes, about 1500 timed plans): the fit picks
-// the measured best plan on 27 of them and is within 3% on all but N = 1000.
+// the measured best plan on 28 of them and is within 3% on all but N = 1000.
 // Per tile: `eff`, the fraction of the fp32 MFMA peak a CU reaches when it is
-// full of such workgroups, and `occ`, the workgroups that share a CU. A work
-// item is one output tile over one K split; the machine runs cus * occ of
-// them per round, so an item count just above a whole number of rounds costs
-// an extra round (4097^3 on 256x256: 289 tiles on 256 CUs); a last round in
-// which each CU holds fewer than occ items runs faster per item, by
-// (held / occ)^PARTIAL_EXP. Splitting K multiplies the items of a problem with
-// few output tiles (768 x 768 x 8192 has 144 on 64x64) and costs the
-// partials' round trip (mostly through the 256 MB last-level cache, hence a
-// rate above HBM's) plus one reduce launch. The model only compares
-// candidates; its times are not predictions.
+// full of such workgroups; per kernel (tile, transposes, epilogue, split or
+// not): the workgroups that fit on a CU, from the runtime's occupancy query
+// (registers and LDS decide it: the 128x128 tile runs 3 per CU, the 64x64
+// tile 5-8). A work item is one output tile over one K split; the machine
+// runs cus * occupancy of them per round, so an item count just above a whole
+// number of rounds costs an extra round (4097^3 on 256x256: 289 tiles on 256
+// CUs); a last round in which each CU holds fewer items than fit runs faster
+// per item, by (held / fit)^PARTIAL_EXP. Splitting K multiplies the items of
+// a problem with few output tiles (768 x 768 x 8192 has 144 on 64x64) and
+// costs the partials' round trip (mostly through the 256 MB last-level
+// cache, hence a rate above HBM's) plus one reduce launch. The model only
+// compares candidates; its times are not predictions.
 enum class TileKind { L, M, N, S };
 struct Cand {
     TileKind kind;
     int bm, bn;
     double eff;
-    int occ;
 };
-constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.89, 1},
-                          {TileKind::M, 128, 128, 0.88, 2},
-                          {TileKind::N, 64, 128, 0.80, 4},
-                          {TileKind::S, 64, 64, 0.80, 6}};
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.909},
+                          {TileKind::M, 128, 128, 0.893},
+                          {TileKind::N, 64, 128, 0.823},
+                          {TileKind::S, 64, 64, 0.809}};
+constexpr int N_CANDS = sizeof(CANDS) / sizeof(CANDS[0]);
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
-constexpr double K_OVERHEAD = 72.0;           // per-item prologue/epilogue, in k steps
-constexpr double PARTIAL_EXP = 0.89;          // speed of a part-filled last round
-constexpr double PARTIALS_BYTES_PER_S = 1.8e13;  // the partials' round trip
-constexpr double LAUNCH_S = 1.4e-6;           // the reduce launch
+constexpr double K_OVERHEAD = 60.0;           // per-item prologue/epilogue, in k steps
+constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last round
+constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
+constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
 constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
 // Largest split-K partial buffer (floats): 256 MiB per host thread and device.
 constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;
+
+// Workgroups per CU of each candidate's kernel: [tile][0 whole K, 1 split-K].
+struct Occupancy {
+    int wgs[N_CANDS][2];
+};
+
+template <class K>
+int wgs_per_cu(K kern, int threads, size_t smem) {
+    bmb::allow_smem(kern, smem);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, smem) != hipSuccess ||
+        n < 1)
+        n = 1;
+    return n;
+}
+
+template <bool TA, bool TB, class Tile, int EPI, bool VEC>
+void tile_occupancy(int (&out)[2]) {
+    using L = bmb::MfmaLayout<TA, TB, Tile>;
+    out[0] = wgs_per_cu(bmb::mfma_gemm_k<TA, TB, Tile, VEC, EPI>, Tile::NT, L::SMEM_BYTES);
+    out[1] = wgs_per_cu(bmb::mfma_gemm_splitk_k<TA, TB, Tile, VEC>, Tile::NT, L::SMEM_BYTES);
+}
 
 struct Plan {
     Cand tile;
@@ -86,18 +111,18 @@ inline int round_up16(long long x) { return (int)((x + 15) / 16 * 16); }
 inline int round_up32(long long x) { return (int)((x + 31) / 32 * 32); }
 
 double model_time(long long M, long long N, long long K, long long batch, const Cand &c,
-                  int splits, int kchunk, int cus) {
+                  int occ, int splits, int kchunk, int cus) {
     const long long tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
     const long long items = tiles * splits;
-    const long long slots = (long long)cus * c.occ;
+    const long long slots = (long long)cus * occ;
     const double peak_cu = 157.3e12 / 256.0;
-    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) / (c.eff * peak_cu) * c.occ;
+    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) / (c.eff * peak_cu) * occ;
     const long long full = items / slots, rem = items % slots;
     double t = full * t_item;
     if (rem) {
-        // A partial round: CUs holding fewer than occ items run each faster.
+        // A partial round: CUs holding fewer items than fit run each faster.
         const long long per_cu = (rem + cus - 1) / cus;
-        t += per_cu < c.occ ? t_item * pow((double)per_cu / c.occ, PARTIAL_EXP) : t_item;
+        t += per_cu < occ ? t_item * pow((double)per_cu / occ, PARTIAL_EXP) : t_item;
     }
     if (splits > 1) t += (splits + 2.0) * M * N * 4.0 / PARTIALS_BYTES_PER_S + LAUNCH_S;
     return t;
@@ -106,11 +131,12 @@ double model_time(long long M, long long N, long long K, long long batch, const 
 // Split-K is used only for single problems on the null stream: its partials
 // live in a per-thread scratch buffer, and only the null stream orders a
 // thread's launches.
-Plan pick(int M, int N, int K, int batch, bool may_split) {
+Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ) {
     const int cus = device_cus();
     Plan best{CANDS[0], 1, round_up16(K)};
     double best_t = -1.0;
-    for (const Cand &c : CANDS) {
+    for (int ci = 0; ci < N_CANDS; ++ci) {
+        const Cand &c = CANDS[ci];
         for (int s : SPLITS) {
             int splits = 1, kchunk = round_up16(K);
             if (s > 1) {
@@ -120,7 +146,8 @@ Plan pick(int M, int N, int K, int batch, bool may_split) {
                 splits = (K + kchunk - 1) / kchunk;
                 if (splits < 2 || (long long)splits * M * N > MAX_SPLIT_FLOATS) continue;
             }
-            const double t = model_time(M, N, K, batch, c, splits, kchunk, cus);
+            const double t =
+                model_time(M, N, K, batch, c, occ.wgs[ci][splits > 1], splits, kchunk, cus);
             if (best_t < 0 || t < best_t) {
                 best_t = t;
                 best = Plan{c, splits, kchunk};
@@ -128,6 +155,31 @@ Plan pick(int M, int N, int K, int batch, bool may_split) {
         }
     }
     return best;
+}
+
+// The occupancy table of one (transposes, epilogue, alignment) case, queried
+// once per device.
+template <bool TA, bool TB, int EPI>
+const Occupancy &occupancy(bool vec) {
+    static Occupancy table[64][2];
+    static std::once_flag once[64][2];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    std::call_once(once[dev][vec], [&] {
+        Occupancy &o = table[dev][vec];
+        if (vec) {
+            tile_occupancy<TA, TB, TileL, EPI, true>(o.wgs[0]);
+            tile_occupancy<TA, TB, TileM, EPI, true>(o.wgs[1]);
+            tile_occupancy<TA, TB, TileN, EPI, true>(o.wgs[2]);
+            tile_occupancy<TA, TB, TileS, EPI, true>(o.wgs[3]);
+        } else {
+            tile_occupancy<TA, TB, TileL, EPI, false>(o.wgs[0]);
+            tile_occupancy<TA, TB, TileM, EPI, false>(o.wgs[1]);
+            tile_occupancy<TA, TB, TileN, EPI, false>(o.wgs[2]);
+            tile_occupancy<TA, TB, TileS, EPI, false>(o.wgs[3]);
+        }
+    });
+    return table[dev][vec];
 }
 
 template <bool TA, bool TB, class Tile, int EPI>
@@ -185,12 +237,13 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const int a_contig = TA ? M : K, b_contig = TB ? K : N;
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && al16(A) && al16(B) &&
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
-    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr);
+    const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
+    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
     float *P = nullptr;
     if (p.splits > 1) {
         P = static_cast<float *>(
             bmb::device_scratch(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float)));
-        if (P == nullptr) p = pick(M, N, K, batch, false);  // no scratch: no split
+        if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
     }
     if (p.splits > 1) {
         switch (p.tile.kind) {
