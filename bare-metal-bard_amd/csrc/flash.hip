@@ -371,7 +371,7 @@ __device__ __forceinline__ void fwd_tile(const float *ks, const float *vs, const
 template <int HS, int WPB, bool SNAKE, int MINW>
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
 flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__restrict__ qkv,
-            int T, int NH, int BH, float qscale, int cus) {
+            int T, int NH, int BH, float qscale, int cus, const unsigned *__restrict__ order) {
     constexpr int NT = WPB * 64, QB = 32 * WPB, HH = HS / 2, DT = HS / 32;
     using S = FwdSmem<HS>;
     extern __shared__ float smem[];
@@ -380,7 +380,13 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
     const int l32 = lane & 31, hf = lane >> 5;
     const int nqb = (T + QB - 1) / QB;
     int qb, bh;
-    work_item<SNAKE>(blockIdx.x, BH, nqb, true, cus, qb, bh);
+    if (order != nullptr) {  // host-planned placement (fwd_order)
+        const unsigned e = order[blockIdx.x];
+        qb = (int)(e & 0xffffu);
+        bh = (int)(e >> 16);
+    } else {
+        work_item<SNAKE>(blockIdx.x, BH, nqb, true, cus, qb, bh);
+    }
     const int b = bh / NH, h = bh % NH, C = NH * HS;
     const size_t rs = 3 * (size_t)C;
     const float *base = qkv + (size_t)b * T * rs + h * HS;
@@ -1078,6 +1084,88 @@ int grid_blocks(int BH, int T, int rows_per_block) {
     return BH * ((T + rows_per_block - 1) / rows_per_block);
 }
 
+// Workgroups of `kern` that fit on one CU at once (0 if unknown).
+template <typename K>
+int wgs_per_cu(K kern, int threads, size_t smem) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, smem) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return per_cu;
+}
+
+// Placement of the forward's (query block, head) items when the whole grid is
+// resident at once. The dispatcher then puts block b on XCD b % 8 and, within
+// an XCD, its local blocks w, w + c, w + 2c, ... (c = CUs per XCD) on the
+// same CU, and the workgroups sharing a CU run side by side until the last
+// one ends: a CU's run time tracks the sum of its items' work (measured
+// correlation 0.93), which the formula order (work_item) left 174-222 key
+// tiles per CU at B=8 H=12 T=1024. Here the items of each XCD's heads (the
+// same heads per XCD as work_item, for L2 reuse) go longest first to the
+// least loaded CU of the XCD that has a free slot; work of an item = the key
+// tiles its waves stream. Entry b = (head << 16) | query block. Built once per
+// (device, shape, occupancy), uploaded (a few KB) and kept until the process
+// ends. nullptr (use the formula order): the grid does not fit at once, B*NH
+// is not a multiple of 8 or above 65535, or the upload fails.
+std::mutex g_fwd_mu;
+std::map<std::tuple<int, int, int, int, int>, unsigned *> g_fwd_order;
+
+const unsigned *fwd_order(int T, int wpb, int BH, int per_cu) {
+    const int QB = 32 * wpb, nqb = (T + QB - 1) / QB, cpx = cus_per_xcd();
+    if (per_cu <= 0 || BH % NXCD != 0 || BH > 65535 || nqb > 65535) return nullptr;
+    const long long nblocks = (long long)nqb * BH;
+    if (nblocks > (long long)cpx * NXCD * per_cu) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    const auto key = std::make_tuple(dev, T, wpb, BH, per_cu);
+    std::lock_guard<std::mutex> lock(g_fwd_mu);
+    const auto found = g_fwd_order.find(key);
+    if (found != g_fwd_order.end()) return found->second;
+
+    const int hpx = BH / NXCD, nx = hpx * nqb;  // heads and items per XCD
+    std::vector<int> cost(nqb);
+    for (int qb = 0; qb < nqb; ++qb) {
+        cost[qb] = 0;
+        for (int w = 0; w < wpb; ++w) {
+            const int q0 = qb * QB + 32 * w;
+            if (q0 < T) cost[qb] += (std::min(T, q0 + 32) + 31) / 32;
+        }
+    }
+    std::vector<unsigned> ent((size_t)nblocks);
+    std::vector<int> order_items(nx), load(cpx), used(cpx), cap(cpx);
+    for (int x = 0; x < NXCD; ++x) {
+        for (int i = 0; i < nx; ++i) order_items[i] = i;  // i = qb * hpx + h
+        std::stable_sort(order_items.begin(), order_items.end(),
+                         [&](int a, int b) { return cost[a / hpx] > cost[b / hpx]; });
+        for (int c = 0; c < cpx; ++c) {
+            load[c] = used[c] = 0;
+            cap[c] = (nx - c + cpx - 1) / cpx;  // local blocks w < nx with w % cpx == c
+        }
+        for (const int i : order_items) {
+            const int qb = i / hpx, h = i % hpx;
+            int best = -1;
+            for (int c = 0; c < cpx; ++c)
+                if (used[c] < cap[c] && (best < 0 || load[c] < load[best])) best = c;
+            const int w = best + used[best] * cpx;
+            ++used[best];
+            load[best] += cost[qb];
+            const int bh = h * NXCD + x;
+            ent[(size_t)w * NXCD + x] = ((unsigned)bh << 16) | (unsigned)qb;
+        }
+    }
+    unsigned *d = nullptr;
+    if (hipMalloc(&d, ent.size() * sizeof(unsigned)) != hipSuccess ||
+        hipMemcpy(d, ent.data(), ent.size() * sizeof(unsigned), hipMemcpyHostToDevice) !=
+            hipSuccess) {
+        (void)hipGetLastError();
+        if (d) (void)hipFree(d);
+        return nullptr;
+    }
+    g_fwd_order[key] = d;
+    return d;
+}
+
 template <int HS, int WPB, bool SNAKE, int MINW>
 void run_fwd(float *out, float *lse, const float *qkv, int B, int T, int NH) {
     const int BH = B * NH;
@@ -1085,8 +1173,10 @@ void run_fwd(float *out, float *lse, const float *qkv, int B, int T, int NH) {
     const size_t smem = FwdSmem<HS>::BYTES;
     auto kern = flash_fwd_k<HS, WPB, SNAKE, MINW>;
     bmb::allow_smem(kern, smem);
+    const unsigned *order =
+        SNAKE ? fwd_order(T, WPB, BH, wgs_per_cu(kern, WPB * 64, smem)) : nullptr;
     bmb::launch(kern, dim3(grid_blocks(BH, T, 32 * WPB)), dim3(WPB * 64), smem, nullptr, out,
-                lse, qkv, T, NH, BH, qscale, cus_per_xcd());
+                lse, qkv, T, NH, BH, qscale, cus_per_xcd(), order);
 }
 
 template <int HS>
@@ -1315,17 +1405,6 @@ bool get_sched(bool kv, int T, int wpb, int BH, int per_cu, Sched &out) {
     g_sched[key] = s;
     out = s;
     return true;
-}
-
-// Workgroups of `kern` that fit on one CU at once (0 if unknown).
-template <typename K>
-int wgs_per_cu(K kern, int threads, size_t smem) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, smem) != hipSuccess) {
-        (void)hipGetLastError();
-        return 0;
-    }
-    return per_cu;
 }
 
 // Kernel of a backward launch mode, with its LDS size allowed.

@@ -23,7 +23,10 @@
  * workgroups on a per-shape work plan that the first backward call of a
  * shape computes on the host and uploads (a few KB per pass, kept per device
  * until the process ends): that first call therefore makes two small
- * allocations and two synchronous copies.
+ * allocations and two synchronous copies. Likewise the default forward
+ * config, when its whole grid fits on the device at once, places its work
+ * by a per-shape order that its first call of a shape uploads (4 bytes per
+ * workgroup: one small allocation and one synchronous copy).
  */
 #ifndef BMB_FLASH_H
 #define BMB_FLASH_H
