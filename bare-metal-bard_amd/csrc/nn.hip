@@ -390,6 +390,31 @@ __global__ __launch_bounds__(NT) void colsum_k(float *partial, const float *dout
     }
 }
 
+// The bias case of colsum_k with 128-bit loads (C % 4 == 0, dout 16-byte
+// aligned): each lane owns 4 adjacent columns and adds its rows in the same
+// order, so every column's partial sum is the same fp32 value as colsum_k's.
+// Four times fewer load instructions; the row loop is unrolled so that
+// several rows' loads are in flight at once.
+__global__ __launch_bounds__(NT) void colsum4_k(float *partial, const float *dout, int N, int C,
+                                                 int rpc) {
+    const int C4 = C / 4;
+    const int c4 = blockIdx.x * NT + threadIdx.x;
+    const int r0 = blockIdx.y * rpc;
+    const int r1 = min(N, r0 + rpc);
+    if (c4 >= C4) return;
+    const float4 *p = reinterpret_cast<const float4 *>(dout) + c4;
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+    for (int r = r0; r < r1; ++r) {
+        const float4 g = p[(size_t)r * C4];
+        s.x += g.x;
+        s.y += g.y;
+        s.z += g.z;
+        s.w += g.w;
+    }
+    reinterpret_cast<float4 *>(partial + (size_t)blockIdx.y * C)[c4] = s;
+}
+
 // dst0[c] += sum_g partial[g][c] for c < C0, dst1[c - C0] += ... for the rest
 // (width columns in all). A workgroup covers FIN_COLS columns with
 // NT / FIN_COLS slices of lanes: slice q sums g = q, q + slices, ... in order,
@@ -920,8 +945,12 @@ void bias_backward(float *dbias, const float *dout, int N, int C) {
     colsum_shape(N, C, rpc, G);
     float *partial = nn_scratch((size_t)G * C);
     if (partial == nullptr) return scratch_failure("bias_backward");
-    bmb::launch(colsum_k<false>, dim3(ceil_div(C, NT), G), dim3(NT), 0, nullptr, partial, dout,
-                nullptr, nullptr, nullptr, N, C, rpc);
+    if (C % 4 == 0 && ((uintptr_t)dout & 15u) == 0)
+        bmb::launch(colsum4_k, dim3(ceil_div(C / 4, NT), G), dim3(NT), 0, nullptr, partial, dout,
+                    N, C, rpc);
+    else
+        bmb::launch(colsum_k<false>, dim3(ceil_div(C, NT), G), dim3(NT), 0, nullptr, partial,
+                    dout, nullptr, nullptr, nullptr, N, C, rpc);
     colsum_finish(dbias, dbias, C, partial, G, C);
 }
 

@@ -171,6 +171,16 @@ def test_bias(gpu, N, C):
         got.append(db.get())
     assert _nw(got[0] - db0, O.bias_bwd(db0, dout, N, C) - db0) < TOL
     assert np.array_equal(got[0], got[1])
+    # The same dout one float off 16-byte alignment takes the 32-bit-load
+    # kernel; every column is summed in the same order, so the bits match.
+    import torch
+    shifted = torch.empty(N * C + 1, device="cuda", dtype=torch.float32)
+    shifted[1:].copy_(dev(dout).reshape(-1))
+    db = Guarded(C, fill=db0)
+    bmb.call("bias_backward", db.ptr, shifted[1:].data_ptr(), N, C)
+    sync("bias_backward misaligned")
+    assert db.ok()
+    assert np.array_equal(db.get(), got[0])
 
 
 @pytest.mark.parametrize("N,V,Vp", [(256, 65, 128), (64, 50257, 50304), (17, 3000, 3001),
