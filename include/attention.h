@@ -21,6 +21,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* src/attention.h:19-20 */
 void attention_forward(float *out, float *qkvr, float *att, const float *qkv,
@@ -32,6 +34,7 @@ void attention_backward(float *dqkv, float *dqkvr, float *datt, float *dpreatt,
                         const float *dout, const float *qkvr, const float *att,
                         int B, int T, int C, int NH);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

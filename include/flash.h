@@ -38,6 +38,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* src/flash.h:36-37. Runs the default config, then any legal config; if none
  * fits the head size, prints a message and calls exit(1) like the reference
@@ -68,6 +70,7 @@ bool flash_attention_backward_cfg(int cfg, float *dqkv, float *dsum,
                                   const float *out, const float *lse, int B,
                                   int T, int C, int NH);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,8 @@ extern "C" {
 #else
 #define BMB_DEFAULT_STREAM
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* src/gemm.h:17-19 (cudaStream_t becomes hipStream_t; 0 = null stream). */
 void gemm(bool transA, bool transB, int M, int N, int K, float alpha,
@@ -40,6 +42,7 @@ void batched_gemm(bool transA, bool transB, int batch, int M, int N, int K,
                   const float *B, long long strideB, float beta, float *C,
                   long long strideC, hipStream_t stream BMB_DEFAULT_STREAM);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

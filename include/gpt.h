@@ -27,6 +27,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* src/gpt.h:10-17 */
 typedef struct GPTConfig {
@@ -129,6 +131,7 @@ int gpt_load_checkpoint(GPT *g, const char *path, char *itos, int itos_cap, int 
 /* A training step is the trainer's sequence (src/train_gpt.cu:395-460):
  * gpt_forward, gpt_backward, grad_global_norm and adamw_update (nn.h). */
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }  /* extern "C" */
 

@@ -14,6 +14,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* src/kernels.h:10-11 */
 typedef void (*sgemm_fn)(int M, int N, int K, float alpha, const float *A,
@@ -64,6 +66,7 @@ void sgemm_mfma_bf16x3(int M, int N, int K, float alpha, const float *A, const f
  * (src/bench.cu:267). */
 int bmb_last_error(void);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

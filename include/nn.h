@@ -27,6 +27,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* Only the declarations below are exported from libbmb.so (built with -fvisibility=hidden). */
+#pragma GCC visibility push(default)
 
 /* ---- embeddings (src/nn.h:10-14) ----
  * out[b,t,:] = wte[tokens[b,t],:] + wpe[t,:]. Token ids must lie in the
@@ -96,6 +98,7 @@ void zero_buffer(float *p, size_t n);
  * on the host. */
 float reduce_mean(const float *d_values, int n);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,7 @@ def _declared():
     for h in HEADERS:
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"^#pragma.*$", "", src, flags=re.M)
         for m in re.finditer(r"\b([A-Za-z_]\w*)\s*\(", src):
             name = m.group(1)
             if name in ("if", "sizeof", "defined", "sgemm_fn", "void") or name.startswith("BMB_"):
@@ -48,6 +49,17 @@ def test_exports_are_c_linkage():
     out = os.popen("nm -D --defined-only %s" % bmb.LIB_PATH).read().split()
     for n in _declared():
         assert n in out, "%s not exported with C linkage" % n
+
+
+def test_exports_nothing_undeclared():
+    """The library's dynamic symbol table is the C ABI of include/*.h: no C++
+    symbol (kernel host stubs, internal helpers, standard-library template
+    instantiations) is visible to a program that links it. The __hip_cuid_*
+    markers are the HIP compiler's per-source identifiers."""
+    rows = [l.split() for l in os.popen("nm -D --defined-only %s" % bmb.LIB_PATH).read().splitlines()]
+    names = {r[-1] for r in rows if len(r) >= 3}
+    extra = sorted(n for n in names - _declared() if not n.startswith("__hip_cuid_"))
+    assert not extra, extra
 
 
 def test_kernel_table():
