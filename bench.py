@@ -253,6 +253,19 @@ def timed_burst(fn, reps, warmup=2):
     return a.elapsed_time(b) / reps
 
 
+def independent_runs(fn, steps, first_ms, runs=3):
+    """The timed region measured `runs` times in all, each with its own
+    warm-up and synchronised ends (the first is the reported one): the
+    per-step ms of each run, their median, and the spread (max - min over
+    the median), flagged above 3%."""
+    ms = [first_ms] + [timed_steps(fn, steps, 2)[0] for _ in range(runs - 1)]
+    s = sorted(ms)
+    med = s[len(s) // 2]
+    spread = 100.0 * (s[-1] - s[0]) / med
+    return {"ms_per_step": [round(x, 4) for x in ms], "median_ms": round(med, 4),
+            "spread_pct": round(spread, 2), "spread_over_3pct": spread > 3.0}
+
+
 def stats(ms):
     s = sorted(ms)
     return {"avg_ms": sum(s) / len(s), "best_ms": s[0], "median_ms": s[len(s) // 2]}
@@ -407,6 +420,7 @@ def main():
                          "frac": round(g / 1e3 / PEAK_FP32_TFLOPS, 4),
                          "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
             "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
+            "independent_runs": independent_runs(sq(args.kernel, N), args.steps, ms),
             "warmup_steps_run": WARM_STEPS_RUN.get("sgemm"),
             "vendor_fp32_gemm_gflops": vendor_sq(torch, dA, dB, dC, N),
             "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
@@ -643,6 +657,7 @@ def flash_bench(args, bmb, O, torch, traffic):
     f_ms, _ = timed_steps(fwd, args.steps, 2)
     b_ms, _ = timed_steps(bwd, args.steps, 2)
     fs, bs = stats(timed(fwd, args.steps, 2)), stats(timed(bwd, args.steps, 2))
+    runs = independent_runs(step, args.steps, tot)
     bmb.check("flash")
     pairs = Bf * NH * T * (T + 1) / 2
     fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
@@ -654,6 +669,7 @@ def flash_bench(args, bmb, O, torch, traffic):
         "ms_fwd": round(f_ms, 4), "ms_bwd": round(b_ms, 4),
         "launch_ms_fwd_median": round(fs["median_ms"], 4),
         "launch_ms_bwd_median": round(bs["median_ms"], 4),
+        "independent_runs": runs,
         "tflops_fwd": round(fwd_fl / f_ms / 1e9, 2),
         "tflops_bwd": round(bwd_fl / b_ms / 1e9, 2),
         "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_TFLOPS, 1),
