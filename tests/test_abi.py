@@ -4,6 +4,8 @@ rejection) behaves like the reference's -- all without touching a GPU."""
 import ctypes
 import os
 import re
+import subprocess
+import sys
 
 import pytest
 
@@ -141,3 +143,12 @@ def test_gpt_param_sizes_and_names():
         assert bmb.param_sizes(cfg) == O.gpt_param_sizes(cfg)
     assert sum(bmb.param_sizes((1024, 50257, 50304, 12, 12, 768))) == 124475904
     assert bmb.param_names() == list(bmb.PARAM_NAMES) == list(O.PARAM_NAMES)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says
+    why, before it touches the GPU or imports torch."""
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
