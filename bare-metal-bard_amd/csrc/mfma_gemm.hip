@@ -76,8 +76,8 @@ constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last rou
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
 constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
-// Largest split-K partial buffer (floats): 256 MiB per host thread and device.
-constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;
+// Largest split-K partial buffer (floats): 640 MiB per host thread and device.
+constexpr long long MAX_SPLIT_FLOATS = 160LL << 20;
 
 // Workgroups per CU of each candidate's kernel: [tile][0 whole K, 1 split-K].
 struct Occupancy {
