@@ -237,9 +237,19 @@ struct MfmaGemm {
                                                                        acc[fi][fn], 0, 0, 0);
     }
 
+    // One 128-bit load of an in-range chunk: an aligned float4 (VEC), or a
+    // 16-byte copy from a 4-byte aligned address, which is still one
+    // global_load_dwordx4 on gfx950 (global loads need only dword alignment).
+    __device__ static __forceinline__ float4 load4_in(const float *p) {
+        if (VEC) return ld4(p);
+        float4 v;
+        __builtin_memcpy(&v, p, sizeof(v));
+        return v;
+    }
+
     // Loads of an interior tile: every row and column of the tile lies inside
     // the operands and K is a whole number of k-tiles, so no chunk needs a
-    // bounds check (aligned 128-bit loads, VEC only).
+    // bounds check and each is one 128-bit load.
     __device__ static __forceinline__ void load_interior(Regs &g, const float *A, const float *B,
                                                          int lda, int ldb, int m0, int n0, int k0,
                                                          int tid) {
@@ -247,15 +257,15 @@ struct MfmaGemm {
         for (int i = 0; i < L::A_PER_T; ++i) {
             int r, c;
             a_chunk(tid + i * NT, r, c);
-            g.a[i] = ld4(TA ? A + (size_t)(k0 + r) * lda + m0 + c
-                            : A + (size_t)(m0 + r) * lda + k0 + c);
+            g.a[i] = load4_in(TA ? A + (size_t)(k0 + r) * lda + m0 + c
+                                 : A + (size_t)(m0 + r) * lda + k0 + c);
         }
 #pragma unroll
         for (int i = 0; i < L::B_PER_T; ++i) {
             int r, c;
             b_chunk(tid + i * NT, r, c);
-            g.b[i] = ld4(TB ? B + (size_t)(n0 + r) * ldb + k0 + c
-                            : B + (size_t)(k0 + r) * ldb + n0 + c);
+            g.b[i] = load4_in(TB ? B + (size_t)(n0 + r) * ldb + k0 + c
+                                 : B + (size_t)(k0 + r) * ldb + n0 + c);
         }
     }
 
@@ -425,15 +435,16 @@ struct MfmaGemm {
         }
     }
 
-    // Picks the interior path when it applies (a uniform branch per workgroup).
+    // Picks the interior path when it applies (a uniform branch per workgroup),
+    // with or without 16-byte aligned operands.
     template <int EPI = EPI_BLAS>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
                                                float alpha, const float *__restrict__ A,
                                                const float *__restrict__ B, float beta,
                                                float *C, int m0, int n0, float *smem,
                                                EpiArgs ep = {}) {
-        if (VEC && m0 + BM <= M && n0 + BN <= N && K > 0 && K % BK == 0)
-            run_tile<EPI, VEC>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+        if (m0 + BM <= M && n0 + BN <= N && K > 0 && K % BK == 0)
+            run_tile<EPI, true>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
         else
             run_tile<EPI, false>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
     }

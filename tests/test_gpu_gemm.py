@@ -53,23 +53,33 @@ def test_gemm_shapes(gpu, shape, trans):
 # interior path's unguarded loads and its prefetch index, clamped to the last
 # k-tile, on every tile size the planner can pick (4096^2 takes 256x256).
 # Small-integer entries (|a|, |b| <= 8, K <= 64) make every fp32 sum exact,
-# so the result must equal the exact product bit for bit.
+# so the result must equal the exact product bit for bit. 1030 x 771 has rows
+# of stored operands that are not whole 16-byte chunks (interior tiles with
+# unaligned rows, plus ragged edge tiles).
 SHORT_K = [(1024, 1024, 16), (512, 768, 32), (2048, 256, 48), (256, 256, 32),
-           (4096, 4096, 32), (768, 192, 64)]
+           (4096, 4096, 32), (768, 192, 64), (1030, 771, 48)]
 
 
+# off = 1: both operands start one float past a 16-byte boundary, so the
+# kernels without aligned 128-bit loads run the same interior tiles with
+# 128-bit loads from 4-byte aligned addresses.
+@pytest.mark.parametrize("off", [0, 1], ids=["aligned", "off1"])
 @pytest.mark.parametrize("trans", TRANS, ids=_tag)
 @pytest.mark.parametrize("shape", SHORT_K, ids=lambda s: "%dx%dx%d" % s)
-def test_interior_short_k_exact(gpu, shape, trans):
+def test_interior_short_k_exact(gpu, shape, trans, off):
+    import torch
     M, N, K = shape
     ta, tb = trans
     r = np.random.default_rng(M + 7 * N + 31 * K)
     A = r.integers(-8, 9, M * K).astype(np.float32)
     B = r.integers(-8, 9, K * N).astype(np.float32)
-    print("gemm exact %s M=%d N=%d K=%d" % (_tag(trans), M, N, K), flush=True)
-    dA, dB = dev(A), dev(B)  # kept alive until the launch has run
+    print("gemm exact %s M=%d N=%d K=%d offset %d" % (_tag(trans), M, N, K, off), flush=True)
+    dA = torch.zeros(A.size + off, device="cuda", dtype=torch.float32)
+    dB = torch.zeros(B.size + off, device="cuda", dtype=torch.float32)
+    dA[off:].copy_(dev(A))  # kept alive until the launch has run
+    dB[off:].copy_(dev(B))
     gC = Guarded(M * N, fill=np.full(M * N, np.nan, np.float32))
-    bmb.gemm(ta, tb, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.0, gC.ptr)
+    bmb.gemm(ta, tb, M, N, K, 1.0, dA[off:].data_ptr(), dB[off:].data_ptr(), 0.0, gC.ptr)
     sync("gemm exact")
     assert gC.ok()
     Am = A.reshape(K, M).T if ta else A.reshape(M, K)
