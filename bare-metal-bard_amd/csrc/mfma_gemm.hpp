@@ -307,17 +307,34 @@ struct MfmaGemm {
         }
     }
 
+    // The loads of k-tile t (k0 = t * BK) for run_tile's MODE: 1 every k-tile
+    // is whole and the tile lies inside M x N (unguarded); 2 the same except
+    // that the last k-tile is cut by K, so its loads are guarded (a uniform
+    // branch); 0 guarded throughout (zero fill past M, N or K).
+    template <int MODE>
+    __device__ static __forceinline__ void load_tile(Regs &g, const float *A, const float *B,
+                                                     int M, int N, int K, int lda, int ldb,
+                                                     int m0, int n0, int t, int nkt, int tid) {
+        if (MODE == 1 || (MODE == 2 && t < nkt - 1))
+            load_interior(g, A, B, lda, ldb, m0, n0, t * BK, tid);
+        else
+            load(g, A, B, M, N, K, lda, ldb, m0, n0, t * BK, tid);
+    }
+
     // One output tile (m0, n0) of one problem over k in [0, K); A and B are
     // positioned at k = 0 of that range, lda / ldb are their row strides.
-    // smem holds two stages. EPI selects what is stored (see Epi). INTERIOR:
-    // the tile lies inside M x N, K % BK == 0 and K > 0 (load_interior).
-    template <int EPI, bool INTERIOR>
+    // smem holds two stages. EPI selects what is stored (see Epi). MODE (see
+    // load_tile): 1 and 2 need the tile inside M x N and K > 0, 1 also
+    // K % BK == 0.
+    template <int EPI, int MODE>
     __device__ static __forceinline__ void run_tile(int M, int N, int K, int lda, int ldb,
                                                     float alpha, const float *__restrict__ A,
                                                     const float *__restrict__ B, float beta,
                                                     float *C, int m0, int n0, float *smem,
                                                     EpiArgs ep) {
         constexpr int G = BK / 8;  // 8-k groups per tile (even)
+        constexpr bool INTERIOR = MODE != 0;             // no M / N bounds checks
+        constexpr bool HINTED = MODE == 1 && HINTS;      // branch-free loop: scheduling hints
         const int tid = threadIdx.x;
         const int wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tile::WAVES_N) * WM;
@@ -335,9 +352,9 @@ struct MfmaGemm {
         if (nkt > 0) {
             Regs g;
             if (INTERIOR) {
-                load_interior(g, A, B, lda, ldb, m0, n0, 0, tid);
+                load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0, 0, nkt, tid);
                 store(g, smem, smem + L::A_SZ, tid);
-                load_interior(g, A, B, lda, ldb, m0, n0, min(1, nkt - 1) * BK, tid);
+                load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0, min(1, nkt - 1), nkt, tid);
             } else {
                 load(g, A, B, M, N, K, lda, ldb, m0, n0, 0, tid);
                 store(g, smem, smem + L::A_SZ, tid);
@@ -368,16 +385,16 @@ struct MfmaGemm {
                         float *nxt = smem + ((kt + 1) & 1) * L::STAGE;
                         store(g, nxt, nxt + L::A_SZ, tid);
                         if (INTERIOR)
-                            load_interior(g, A, B, lda, ldb, m0, n0, min(kt + 2, nkt - 1) * BK,
-                                          tid);
+                            load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0,
+                                            min(kt + 2, nkt - 1), nkt, tid);
                         else
                             load(g, A, B, M, N, K, lda, ldb, m0, n0, (kt + 2) * BK, tid);
-                        if (INTERIOR && HINTS) hint_before_barrier();
+                        if (HINTED) hint_before_barrier();
                         __syncthreads();
                         fragments(nxt, nxt + L::A_SZ, 0, wm, wn, lane, fa[cb ^ 1], fb[cb ^ 1]);
                     }
                     mma(fa[cb], fb[cb], acc);
-                    if (INTERIOR && HINTS && grp == G - 1) hint_after_barrier();
+                    if (HINTED && grp == G - 1) hint_after_barrier();
                 }
             }
         }
@@ -436,17 +453,22 @@ struct MfmaGemm {
     }
 
     // Picks the interior path when it applies (a uniform branch per workgroup),
-    // with or without 16-byte aligned operands.
+    // with or without 16-byte aligned operands; a K that is not a whole number
+    // of k-tiles guards only the last k-tile's loads.
     template <int EPI = EPI_BLAS>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
                                                float alpha, const float *__restrict__ A,
                                                const float *__restrict__ B, float beta,
                                                float *C, int m0, int n0, float *smem,
                                                EpiArgs ep = {}) {
-        if (m0 + BM <= M && n0 + BN <= N && K > 0 && K % BK == 0)
-            run_tile<EPI, true>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
-        else
-            run_tile<EPI, false>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+        if (m0 + BM <= M && n0 + BN <= N && K > 0) {
+            if (K % BK == 0)
+                run_tile<EPI, 1>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+            else
+                run_tile<EPI, 2>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+        } else {
+            run_tile<EPI, 0>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+        }
     }
 };
 

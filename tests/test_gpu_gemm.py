@@ -55,9 +55,11 @@ def test_gemm_shapes(gpu, shape, trans):
 # Small-integer entries (|a|, |b| <= 8, K <= 64) make every fp32 sum exact,
 # so the result must equal the exact product bit for bit. 1030 x 771 has rows
 # of stored operands that are not whole 16-byte chunks (interior tiles with
-# unaligned rows, plus ragged edge tiles).
+# unaligned rows, plus ragged edge tiles). K = 40 and 63 end in a partial
+# k-tile: interior tiles guard only that k-tile's loads.
 SHORT_K = [(1024, 1024, 16), (512, 768, 32), (2048, 256, 48), (256, 256, 32),
-           (4096, 4096, 32), (768, 192, 64), (1030, 771, 48)]
+           (4096, 4096, 32), (768, 192, 64), (1030, 771, 48), (1024, 1024, 40),
+           (2048, 512, 63), (4096, 4096, 8)]
 
 
 # off = 1: both operands start one float past a 16-byte boundary, so the
