@@ -55,6 +55,7 @@
 #include <functional>
 #include <map>
 #include <mutex>
+#include <optional>
 #include <tuple>
 #include <vector>
 
@@ -1070,15 +1071,11 @@ const BwdCfg BWD_CFGS[] = {
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
 constexpr int BWD_DEFAULT = 5;
 
-// dS workspace: one buffer per device, grown on demand and kept until the
-// process ends. Growing waits for the device to go idle first, because
-// earlier launches on any stream may still read the old buffer. Calls on one
-// device share the buffer, so backward calls that run concurrently on two
-// streams of one device race on it (the reference's backward runs on the
-// null stream, where launches are serialised).
-float *ds_workspace(size_t bytes) {
-    return static_cast<float *>(bmb::device_scratch(bmb::SCRATCH_FLASH_DS, bytes));
-}
+// dS workspace: leased from the library's per-device pool for one backward
+// call (workspace.hpp). Both passes that use it are queued on the null stream
+// within the call, so a buffer that goes back to the pool is only reused by
+// launches that run after them; concurrent calls from several host threads
+// hold buffers of their own.
 
 int grid_blocks(int BH, int T, int rows_per_block) {
     return BH * ((T + rows_per_block - 1) / rows_per_block);
@@ -1432,6 +1429,7 @@ template <int HS, int WPB, int MINW>
 bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const float *qkv,
              const float *out, const float *lse, int B, int T, int NH) {
     float *ws = nullptr;
+    std::optional<bmb::ScratchLease> lease;
     Sched kv_sc, q_sc;
     kv_sc.items.n = q_sc.items.n = 0;
     const int BH = B * NH;
@@ -1443,7 +1441,9 @@ bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const
             !get_sched(false, T, WPB, BH,
                        wgs_per_cu(bwd_kernel<HS, WPB, 4, MINW>(), threads, smem), q_sc))
             return false;
-        ws = ds_workspace((size_t)B * NH * ds_tiles_per_head(T) * 1024 * sizeof(float));
+        lease.emplace(bmb::SCRATCH_FLASH_DS,
+                      (size_t)B * NH * ds_tiles_per_head(T) * 1024 * sizeof(float));
+        ws = static_cast<float *>(lease->get());
         if (ws == nullptr) return false;  // no workspace: the caller tries another config
     }
     const unsigned long long kv_zero = kv_sc.zero_mask, q_zero = q_sc.zero_mask;

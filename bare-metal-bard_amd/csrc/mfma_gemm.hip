@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <optional>
 
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
@@ -76,7 +77,7 @@ constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last rou
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
 constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
-// Largest split-K partial buffer (floats): 640 MiB per host thread and device.
+// Largest split-K partial buffer (floats): 640 MiB per call in flight on a device.
 constexpr long long MAX_SPLIT_FLOATS = 160LL << 20;
 
 // Workgroups per CU of each candidate's kernel: [tile][0 whole K, 1 split-K].
@@ -88,9 +89,11 @@ template <class K>
 int wgs_per_cu(K kern, int threads, size_t smem) {
     bmb::allow_smem(kern, smem);
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, smem) != hipSuccess ||
-        n < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, smem) != hipSuccess) {
+        (void)hipGetLastError();  // the next launch must not report this query's failure
         n = 1;
+    }
+    if (n < 1) n = 1;
     return n;
 }
 
@@ -129,8 +132,7 @@ double model_time(long long M, long long N, long long K, long long batch, const 
 }
 
 // Split-K is used only for single problems on the null stream: its partials
-// live in a per-thread scratch buffer, and only the null stream orders a
-// thread's launches.
+// live in leased scratch, whose reuse is ordered by the null stream.
 Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ) {
     const int cus = device_cus();
     Plan best{CANDS[0], 1, round_up16(K)};
@@ -240,9 +242,10 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
     Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
     float *P = nullptr;
+    std::optional<bmb::ScratchLease> lease;
     if (p.splits > 1) {
-        P = static_cast<float *>(
-            bmb::device_scratch(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float)));
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
+        P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
     }
     if (p.splits > 1) {

@@ -16,6 +16,7 @@
 //     shape, so every result is the same bit pattern on every call.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -759,13 +760,13 @@ __global__ __launch_bounds__(NT) void sum_k(double *partial, const float *x, lon
 }
 
 // ------------------------------------------------------------------ host side
-float *nn_scratch(size_t floats) {
-    return static_cast<float *>(bmb::device_scratch(bmb::SCRATCH_NN, floats * sizeof(float)));
-}
-
-void scratch_failure(const char *what) {
+// The partial sums of a reduction live in a buffer leased for the call
+// (workspace.hpp). A void op that cannot get one stops the process, as the
+// reference's CUDA_CHECK does on any CUDA error (src/gpt.cu:18-26): returning
+// would leave its gradients unwritten with nothing to tell the caller.
+[[noreturn]] void scratch_failure(const char *what) {
     fprintf(stderr, "bmb: %s: cannot allocate the reduction scratch buffer\n", what);
-    bmb::note_launch_status(hipErrorOutOfMemory);
+    exit(1);
 }
 
 // Number of float4 chunks per lane for the register-resident row kernels.
@@ -893,8 +894,9 @@ void layernorm_backward(float *dinp, float *dweight, float *dbias, const float *
         const int G0 = std::max(1, std::min(256, ceil_div(N, LN_WAVES)));
         const int rpb = ceil_div(ceil_div(N, G0), LN_WAVES) * LN_WAVES;
         const int G = ceil_div(N, rpb);
-        float *partial = nn_scratch((size_t)G * 2 * C);
-        if (partial == nullptr) return scratch_failure("layernorm_backward");
+        bmb::ScratchLease ws(bmb::SCRATCH_NN, (size_t)G * 2 * C * sizeof(float));
+        if (!ws) scratch_failure("layernorm_backward");
+        float *partial = static_cast<float *>(ws.get());
         switch (nch) {
             case 1: ln_bwd_launch<1>(dinp, partial, dout, inp, weight, mean, rstd, N, C, rpb, G); break;
             case 2: ln_bwd_launch<2>(dinp, partial, dout, inp, weight, mean, rstd, N, C, rpb, G); break;
@@ -906,8 +908,9 @@ void layernorm_backward(float *dinp, float *dweight, float *dbias, const float *
     }
     int rpc, G;
     colsum_shape(N, C, rpc, G);
-    float *partial = nn_scratch((size_t)G * 2 * C);
-    if (partial == nullptr) return scratch_failure("layernorm_backward");
+    bmb::ScratchLease ws(bmb::SCRATCH_NN, (size_t)G * 2 * C * sizeof(float));
+    if (!ws) scratch_failure("layernorm_backward");
+    float *partial = static_cast<float *>(ws.get());
     bmb::launch(ln_bwd_dx_generic_k, dim3(ceil_div(N, NT / 64)), dim3(NT), 0, nullptr, dinp,
                 dout, inp, weight, mean, rstd, N, C);
     bmb::launch(colsum_k<true>, dim3(ceil_div(C, NT), G), dim3(NT), 0, nullptr, partial, dout,
@@ -943,8 +946,9 @@ void bias_backward(float *dbias, const float *dout, int N, int C) {
     if (N <= 0 || C <= 0) return;
     int rpc, G;
     colsum_shape(N, C, rpc, G);
-    float *partial = nn_scratch((size_t)G * C);
-    if (partial == nullptr) return scratch_failure("bias_backward");
+    bmb::ScratchLease ws(bmb::SCRATCH_NN, (size_t)G * C * sizeof(float));
+    if (!ws) scratch_failure("bias_backward");
+    float *partial = static_cast<float *>(ws.get());
     if (C % 4 == 0 && ((uintptr_t)dout & 15u) == 0)
         bmb::launch(colsum4_k, dim3(ceil_div(C / 4, NT), G), dim3(NT), 0, nullptr, partial, dout,
                     N, C, rpc);
@@ -991,12 +995,13 @@ void adamw_update(float *params, float *grads, float *m, float *v, int n, float 
 
 float grad_global_norm(const float *grads, int n) {
     if (n <= 0) return 0.0f;
-    void *ws = bmb::device_scratch(bmb::SCRATCH_NN, NORM_BLOCKS * sizeof(double) + 256);
-    if (ws == nullptr) {
-        scratch_failure("grad_global_norm");
+    bmb::ScratchLease ws(bmb::SCRATCH_NN, NORM_BLOCKS * sizeof(double) + 256);
+    if (!ws) {
+        fprintf(stderr, "bmb: grad_global_norm: cannot allocate the reduction scratch buffer\n");
+        bmb::note_launch_status(hipErrorOutOfMemory);
         return NAN;
     }
-    double *partial = static_cast<double *>(ws);
+    double *partial = static_cast<double *>(ws.get());
     float *out = reinterpret_cast<float *>(partial + NORM_BLOCKS);
     const int blocks = (int)std::max(1LL, std::min<long long>(NORM_BLOCKS, (n / 4 + NT - 1) / NT));
     bmb::launch(sumsq_k, dim3(blocks), dim3(NT), 0, nullptr, partial, grads, (long long)n);
@@ -1009,12 +1014,13 @@ void zero_buffer(float *p, size_t n) { run_map(Zero{p}, (long long)n); }
 
 float reduce_mean(const float *d_values, int n) {
     if (n <= 0) return NAN;
-    void *ws = bmb::device_scratch(bmb::SCRATCH_NN, NORM_BLOCKS * sizeof(double) + 256);
-    if (ws == nullptr) {
-        scratch_failure("reduce_mean");
+    bmb::ScratchLease ws(bmb::SCRATCH_NN, NORM_BLOCKS * sizeof(double) + 256);
+    if (!ws) {
+        fprintf(stderr, "bmb: reduce_mean: cannot allocate the reduction scratch buffer\n");
+        bmb::note_launch_status(hipErrorOutOfMemory);
         return NAN;
     }
-    double *partial = static_cast<double *>(ws);
+    double *partial = static_cast<double *>(ws.get());
     float *out = reinterpret_cast<float *>(partial + NORM_BLOCKS);
     const int blocks = (int)std::max(1LL, std::min<long long>(NORM_BLOCKS, ((long long)n + NT - 1) / NT));
     bmb::launch(sum_k, dim3(blocks), dim3(NT), 0, nullptr, partial, d_values, (long long)n);

@@ -219,12 +219,7 @@ template <bool VEC>
 void launch_nn(int M, int N, int K, float alpha, const float *A, const float *B,
                float beta, float *C) {
     auto kern = bf16x3_k<false, false, VEC>;
-    static bool configured = [&] {
-        return hipFuncSetAttribute((const void *)kern,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)SMEM_BYTES) == hipSuccess;
-    }();
-    (void)configured;
+    bmb::allow_smem(kern, SMEM_BYTES);
     const int tiles_m = bmb::ceil_div(M, BM), tiles_n = bmb::ceil_div(N, BN);
     bmb::launch(kern, dim3(tiles_m * tiles_n), dim3(NT), SMEM_BYTES, nullptr, M,
                 N, K, alpha, A, B, beta, C, tiles_m, tiles_n);

@@ -1,43 +1,88 @@
-// Per-device grow-only scratch buffers (see workspace.hpp).
+// Per-device pools of leased scratch buffers (see workspace.hpp).
 #include "workspace.hpp"
 
 #include <hip/hip_runtime_api.h>
 
+#include <mutex>
+#include <vector>
 
 namespace bmb {
 
+struct ScratchBuffer {
+    void *ptr = nullptr;
+    size_t cap = 0;
+};
+
 namespace {
 constexpr int MAX_DEVICES = 64;
-// Per host thread: kernels a thread queues on the null stream run in its
-// order, so one thread's calls never overlap on its own buffers, and two
-// threads never share one.
-thread_local void *g_ptr[MAX_DEVICES][SCRATCH_SLOTS] = {};
-thread_local size_t g_cap[MAX_DEVICES][SCRATCH_SLOTS] = {};
+
+struct Pool {
+    std::mutex mu;
+    std::vector<ScratchBuffer *> idle;  // buffers not leased right now
+};
+
+// Never destroyed: a thread may still return a lease while the process exits.
+Pool &pool(int dev, ScratchSlot slot) {
+    static Pool *pools = new Pool[MAX_DEVICES * SCRATCH_SLOTS];
+    return pools[dev * SCRATCH_SLOTS + slot];
+}
 }  // namespace
 
-void *device_scratch(ScratchSlot slot, size_t bytes) {
+ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes) : slot_(slot) {
     int dev = 0;
-    if (slot < 0 || slot >= SCRATCH_SLOTS) return nullptr;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
-    if (bytes == 0) bytes = 256;
-    void *&ptr = g_ptr[dev][slot];
-    size_t &cap = g_cap[dev][slot];
-    if (cap < bytes) {
-        if (ptr != nullptr) {
-            if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-            (void)hipFree(ptr);
-            ptr = nullptr;
-            cap = 0;
-        }
-        void *p = nullptr;
-        if (hipMalloc(&p, bytes) != hipSuccess) {
-            (void)hipGetLastError();  // clear the allocation failure
-            return nullptr;
-        }
-        ptr = p;
-        cap = bytes;
+    if (slot < 0 || slot >= SCRATCH_SLOTS) return;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        (void)hipGetLastError();
+        return;
     }
-    return ptr;
+    if (bytes == 0) bytes = 256;
+    Pool &p = pool(dev, slot);
+    {
+        // The smallest idle buffer that fits; else the largest idle one, to
+        // grow; else a new one.
+        std::lock_guard<std::mutex> lock(p.mu);
+        int fit = -1, big = -1;
+        for (int i = 0; i < (int)p.idle.size(); ++i) {
+            const size_t c = p.idle[i]->cap;
+            if (c >= bytes && (fit < 0 || c < p.idle[fit]->cap)) fit = i;
+            if (big < 0 || c > p.idle[big]->cap) big = i;
+        }
+        const int pick = fit >= 0 ? fit : big;
+        if (pick >= 0) {
+            buf_ = p.idle[pick];
+            p.idle.erase(p.idle.begin() + pick);
+        } else {
+            buf_ = new ScratchBuffer;
+        }
+    }
+    dev_ = dev;
+    if (buf_->cap < bytes) {
+        if (buf_->ptr != nullptr) {
+            // Work queued by an earlier lessee may still read the old buffer.
+            if (hipDeviceSynchronize() != hipSuccess) {
+                (void)hipGetLastError();
+                return;  // the destructor puts the buffer back unchanged
+            }
+            (void)hipFree(buf_->ptr);
+            buf_->ptr = nullptr;
+            buf_->cap = 0;
+        }
+        void *q = nullptr;
+        if (hipMalloc(&q, bytes) != hipSuccess) {
+            (void)hipGetLastError();  // clear the allocation failure
+            return;
+        }
+        buf_->ptr = q;
+        buf_->cap = bytes;
+    }
+    ptr_ = buf_->ptr;
+}
+
+ScratchLease::~ScratchLease() {
+    if (buf_ == nullptr) return;
+    Pool &p = pool(dev_, slot_);
+    std::lock_guard<std::mutex> lock(p.mu);
+    p.idle.push_back(buf_);
 }
 
 }  // namespace bmb

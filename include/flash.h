@@ -14,12 +14,16 @@
  *
  * Memory: the default backward config stores the causal 32x32 tiles of dS
  * (fp32, 4 KiB each, B*NH*n(n+1)/2 of them with n = ceil(T/32)) in a
- * library-owned per-device workspace, allocated on first use, grown on
- * demand and kept until the process ends. If it cannot be allocated the
- * backward falls back to a config that recomputes S and dP instead and
- * allocates nothing; flash_attention_backward_cfg can select such a config
- * directly. Concurrent backward calls on two streams of one device share the
- * workspace and must be serialised. The same configs run as persistent
+ * workspace that each call leases from a library-owned pool of the device
+ * and returns once it has queued its work; the pool keeps its buffers for
+ * reuse until the process ends and holds as many as were ever leased at once
+ * (one per concurrently calling host thread), however many threads come and
+ * go. All of it runs on the null stream, where launches from every host
+ * thread run in submission order, so the next call to lease a buffer runs
+ * after the last one that used it. If it cannot be allocated the backward
+ * falls back to a config that recomputes S and dP instead and allocates
+ * nothing; flash_attention_backward_cfg can select such a config directly.
+ * The same configs run as persistent
  * workgroups on a per-shape work plan that the first backward call of a
  * shape computes on the host and uploads (a few KB per pass, kept per device
  * until the process ends): that first call therefore makes two small

@@ -13,9 +13,11 @@
  * on the shape, so repeated calls on the same inputs give the same bits. The
  * reference uses atomics for the layernorm weight/bias and the embedding
  * gradients (src/nn.cu:44-45,108-109); this library reduces the layernorm and
- * bias gradients through per-block partial sums in a library-owned scratch
- * buffer (per host thread and device; a few MB at GPT-2 sizes, allocated on
- * first use and kept until the process ends) and the token-embedding
+ * bias gradients through per-block partial sums in a scratch buffer that the
+ * call leases from a library-owned pool of the device (a few MB at GPT-2
+ * sizes; the pool keeps one buffer per concurrently calling host thread until
+ * the process ends; a void op that cannot allocate it prints an error and
+ * exits, as any CUDA error does in the reference) and the token-embedding
  * gradient by letting the first position of each token id sum all its
  * positions in order.
  */
