@@ -103,6 +103,37 @@ def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- GEMM
+def bf16_rne(x) -> np.ndarray:
+    """fp32 -> the nearest bfloat16 (ties to even), returned as fp32 values.
+    Finite inputs only. Rounds the 32-bit pattern at bit 16: add 0x7FFF plus
+    the lowest kept bit, then clear the low half."""
+    u = _c(x).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
+def bf16x3_split(x):
+    """(hi, lo) of the bf16x3 scheme of KERNELS id 10: hi = bf16(x),
+    lo = bf16(x - hi); x - hi is exact in fp32 (hi holds x's leading bits)."""
+    x = _c(x)
+    hi = bf16_rne(x)
+    lo = bf16_rne(x - hi)
+    return hi, lo
+
+
+def gemm_bf16x3_f64(M, N, K, alpha, A, B, beta, C0):
+    """What KERNELS id 10 computes, with exact sums: alpha * (Ah Bh + Ah Bl +
+    Al Bh) + beta * C0 in fp64 (row-major A M x K, B K x N). Products of two
+    bfloat16 are exact in fp64 and the fp64 sums are ~K 2^-53 from exact, so
+    the GPU result differs from this only by its fp32 accumulation."""
+    Ah, Al = (v.astype(np.float64).reshape(M, K) for v in bf16x3_split(A))
+    Bh, Bl = (v.astype(np.float64).reshape(K, N) for v in bf16x3_split(B))
+    out = alpha * (Ah @ Bh + Ah @ Bl + Al @ Bh)
+    if beta != 0:
+        out += beta * _c(C0, np.float64).reshape(M, N)
+    return out
+
+
 def gemm_f32seq(ta, tb, M, N, K, alpha, A, B, beta, C0, threads: int = 1):
     """Returns the new C (a copy); C0 is the C read when beta != 0."""
     C = _c(C0).copy() if C0 is not None else np.zeros(M * N, np.float32)

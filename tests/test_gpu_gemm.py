@@ -114,20 +114,24 @@ def test_batched_gemm(gpu, bshape, trans):
     assert bad == 0 and err < 1e-4
 
 
-GPT = [  # (M, N, K, ta, tb, beta): forward NT, backward dX = NN, dW = TN (beta 1)
-    (8192, 2304, 768, False, True, 0.0), (8192, 768, 768, False, True, 0.0),
-    (8192, 3072, 768, False, True, 0.0), (8192, 768, 3072, False, True, 0.0),
-    (8192, 50257, 768, False, True, 0.0),
-    (8192, 768, 2304, False, False, 0.0), (8192, 768, 3072, False, False, 0.0),
-    (2304, 768, 8192, True, False, 1.0), (768, 3072, 8192, True, False, 1.0),
-    (50257, 768, 8192, True, False, 1.0),
-]
+# the 15 GEMMs of the GPT-2-small step (BT = 8192,
+# C = 768, V = 50257), i.e. every (layer, pass) that bench.py times. Layer
+# (cin, cout): forward y = x w^T is NT (BT, cout, cin); dX = dy w is NN
+# (BT, cin, cout); dW += dy^T x is TN (cout, cin, BT) with beta 1
+# (src/gpt.cu:256-376).
+_LAYERS = [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257)]
+GPT = ([(8192, co, ci, False, True, 0.0) for ci, co in _LAYERS] +
+       [(8192, ci, co, False, False, 0.0) for ci, co in _LAYERS] +
+       [(co, ci, 8192, True, False, 1.0) for ci, co in _LAYERS])
 
 
 @pytest.mark.parametrize("g", GPT, ids=lambda g: "%dx%dx%d_%s" % (g[0], g[1], g[2], _tag(g[3:5])))
 def test_gpt_training_shapes(gpu, g):
     """BASELINE config 3 shapes (weights N(0, 0.02^2), activations N(0, 1)),
-    checked on a sample of output rows (rows are independent problems)."""
+    checked on a sample of output rows (rows are independent problems). The
+    ragged LM head at V = 50257 runs split over K in the dX NN case (K =
+    50257 ends in a partial k-tile, rows not 16-byte aligned) and over 2-D
+    tiles with a ragged edge in the forward and dW."""
     M, N, K, ta, tb, beta = g
     A = O.fill_normal(M * K, 0xA11CE, 1.0)
     B = O.fill_normal(K * N, 0xB0B, 0.02)

@@ -75,18 +75,41 @@ def test_mfma_within_tol(gpu, kid, shape):
     assert err < bmb.find_kernel(kid)["tol"]
     if kid == 9:  # fp32 products: only the summation order differs
         assert err < fp32_order_bound(K)
+    if kid == 10:
+        _check_bf16x3(got, M, N, K, 0.5, A, B, 3.0, C0)
+
+
+def _check_bf16x3(got, M, N, K, alpha, A, B, beta, C0):
+    """id 10's derived bound: the result is the bf16x3 split's exact value
+    (oracle.gemm_bf16x3_f64: three bf16 x bf16 products per term, each exact
+    in fp32) up to fp32 accumulation of 3K terms, so it is held to the
+    summation-order bound of 3K adds around that value. A dropped or doubled
+    cross term or a truncating split misses it by orders of magnitude; the
+    split's own error against the exact product (2^-16 |a b| per product at
+    most) is printed beside it."""
+    want = O.gemm_bf16x3_f64(M, N, K, alpha, A, B, beta, C0)
+    err, bad = O.normwise(got, want)
+    exact = O.normwise(want.astype(np.float32), O.gemm_f64(0, 0, M, N, K, alpha, A, B, beta, C0))[0]
+    print("id 10: normwise %.2e around the bf16x3 value (bound %.2e); split vs exact %.2e"
+          % (err, fp32_order_bound(3 * K), exact))
+    assert bad == 0 and err < fp32_order_bound(3 * K)
+
+
+SWEEP_N = [512, 1000, 1024, 1536, 2048, 4096, 4097, 6144, 8192]  # BASELINE config 2
 
 
 @pytest.mark.parametrize("kid", [8, 9, 10])
-@pytest.mark.parametrize("n", [4096, 4097])
+@pytest.mark.parametrize("n", SWEEP_N)
 def test_large_sampled_rows(gpu, kid, n):
-    """BASELINE sizes; rows are independent, so a row sample of the oracle
-    checks the full-size launch (incl. the ragged 4097 edge rows)."""
+    """BASELINE config 2, every size the bench sweeps: alpha = 1, beta = 0.5,
+    C pre-filled, the bench's seeds (src/bench.cu:226-228). Rows are
+    independent problems, so a row sample of the oracle checks the full-size
+    launch (incl. the ragged edge rows of 1000 and 4097)."""
     M = N = K = n
     A, B, C0 = _inputs(M, N, K)
     got = _run(kid, M, N, K, 1.0, 0.5, A, B, C0)
-    rows = np.unique(np.r_[0, 1, 127, 128, 255, 256, 1000, n // 2, n - 129, n - 2, n - 1,
-                           np.random.default_rng(7).integers(0, n, 8)])
+    rows = np.unique(np.r_[0, 1, 127, 128, 255, 256, min(1000, n - 1), n // 2, n - 129, n - 2,
+                           n - 1, np.random.default_rng(7).integers(0, n, 8)])
     As = A[rows]
     ref = O.gemm_f64(0, 0, len(rows), N, K, 1.0, As, B, 0.5, C0[rows])
     err, bad = O.normwise(got[rows], ref)
@@ -94,6 +117,10 @@ def test_large_sampled_rows(gpu, kid, n):
     if kid == 8:
         want = O.gemm_f32seq(0, 0, len(rows), N, K, 1.0, As, B, 0.5, C0[rows], threads=0)
         assert np.array_equal(got[rows], want)
+    if kid == 9:
+        assert err < fp32_order_bound(K)
+    if kid == 10:
+        _check_bf16x3(got[rows], len(rows), N, K, 1.0, As, B, 0.5, C0[rows])
 
 
 @pytest.mark.parametrize("kid", VALU_IDS + MFMA_IDS)

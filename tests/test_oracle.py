@@ -324,3 +324,23 @@ def test_golden_attention():
     assert np.allclose(l, z["lse"], rtol=1e-12, atol=1e-13)
     g = O.attn_bwd_f64(z["qkv"], z["dout"], B, T, C, NH)
     assert np.allclose(g, z["dqkv"], rtol=1e-10, atol=1e-12)
+
+
+def test_bf16_rne_matches_torch():
+    """The oracle's fp32 -> bfloat16 rounding (used to restate KERNELS id 10)
+    equals torch's conversion, which rounds to nearest even: random values,
+    exact ties (the halfway pattern 0x8000 with an even and an odd kept bit),
+    carries into the exponent, subnormals, signed zeros."""
+    import torch
+    r = np.random.default_rng(10)
+    x = np.concatenate([
+        r.standard_normal(100000).astype(np.float32),
+        (r.standard_normal(1000) * 1e-39).astype(np.float32),
+        np.array([0x3F808000, 0x3F818000, 0x3F7FFFFF, 0x3FFF8000, 0x80000000, 0,
+                  0x00008000, 0x00018000], np.uint32).view(np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(O.bf16_rne(x).view(np.uint32), want.view(np.uint32))
+    hi, lo = O.bf16x3_split(x)
+    assert np.array_equal((x - hi) + hi, x)  # x - hi is exact in fp32
+    big = np.abs(x) > 1e-30
+    assert (np.abs(x - hi - lo)[big] <= np.abs(x)[big] * 2.0 ** -16).all()
