@@ -94,6 +94,8 @@ _SIGS = {
                     c_float, c_vp, c_vp]),
     "batched_gemm": (None, [c_bool, c_bool, c_int, c_int, c_int, c_int, c_float,
                             c_vp, c_ll, c_vp, c_ll, c_float, c_vp, c_ll, c_vp]),
+    "gemm_noalloc": (c_int, [c_bool, c_bool, c_int, c_int, c_int, c_float, c_vp, c_vp,
+                             c_float, c_vp, c_vp]),
     # flash.h
     "flash_attention_forward": (None, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int]),
     "flash_attention_backward": (None, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,

@@ -8,6 +8,7 @@
 // host picks the tile size and a split of K (pick()) and whether every row of
 // the operands is 16-byte aligned.
 #include <math.h>
+#include <stdio.h>
 
 #include <algorithm>
 #include <mutex>
@@ -80,6 +81,46 @@ constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may ge
 // Largest split-K partial buffer (floats): 640 MiB per call in flight on a device.
 constexpr long long MAX_SPLIT_FLOATS = 160LL << 20;
 
+}  // namespace
+
+// Split-K partials of gemm_noalloc(): a fixed array of device memory instead
+// of leased scratch (64 MiB; every GPU that loads this code object holds its
+// own copy until the process ends). Host code never passes `scratch` itself
+// to a kernel -- on the host that name is only a stand-in -- but the device
+// address hipGetSymbolAddress returns for the current device.
+constexpr long long NOALLOC_SPLIT_FLOATS = 16LL << 20;
+static __device__ __align__(256) float scratch[NOALLOC_SPLIT_FLOATS];
+
+namespace {
+
+// The address of the current device's `scratch`, resolved on the first call
+// on that device (with it current) and kept; nullptr (with a message) if the
+// runtime cannot give it.
+float *noalloc_scratch() {
+    constexpr int MAX_DEV = 64;
+    static std::mutex mu;
+    static float *addr[MAX_DEV] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
+        (void)hipGetLastError();
+        fprintf(stderr, "gemm_noalloc: no current device (or more than %d devices)\n", MAX_DEV);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        float *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            fprintf(stderr, "gemm_noalloc: cannot resolve the scratch array on device %d: %s\n",
+                    dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
 // Workgroups per CU of each candidate's kernel: [tile][0 whole K, 1 split-K].
 struct Occupancy {
     int wgs[N_CANDS][2];
@@ -131,9 +172,11 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     return t;
 }
 
-// Split-K is used only for single problems on the null stream: its partials
-// live in leased scratch, whose reuse is ordered by the null stream.
-Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ) {
+// Split-K is used only for single problems, and for gemm() only on the null
+// stream: its partials live in leased scratch, whose reuse is ordered by the
+// null stream. max_floats caps the partials (splits * M * N).
+Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
+          long long max_floats = MAX_SPLIT_FLOATS) {
     const int cus = device_cus();
     Plan best{CANDS[0], 1, round_up16(K)};
     double best_t = -1.0;
@@ -146,7 +189,7 @@ Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ) 
                 kchunk = round_up32((K + s - 1) / s);  // whole k-tiles of every tile's BK
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
-                if (splits < 2 || (long long)splits * M * N > MAX_SPLIT_FLOATS) continue;
+                if (splits < 2 || (long long)splits * M * N > max_floats) continue;
             }
             const double t =
                 model_time(M, N, K, batch, c, occ.wgs[ci][splits > 1], splits, kchunk, cus);
@@ -208,31 +251,37 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
 // one reduce kernel adds them in range order and applies the epilogue.
 template <bool TA, bool TB, class Tile, int EPI>
 void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *A,
-                  const float *B, float beta, float *C, float *P, bool vec, bmb::EpiArgs ep) {
+                  const float *B, float beta, float *C, float *P, bool vec, bmb::EpiArgs ep,
+                  hipStream_t stream) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, p.splits);
     if (vec) {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, nullptr, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
     } else {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, nullptr, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
     }
     const long long mn = (long long)M * N;
     bmb::launch(bmb::splitk_reduce_k<EPI>, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
-                nullptr, C, (const float *)P, p.splits, mn, N, alpha, beta, ep);
+                stream, C, (const float *)P, p.splits, mn, N, alpha, beta, ep);
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// fixed: the split-K partials go to `fixed` (NOALLOC_SPLIT_FLOATS floats, the
+// gemm_noalloc() array) on any stream, instead of leased scratch on the null
+// stream only. Returns false, with nothing launched, only if a plan's
+// partials would not fit there (the planner never picks such a plan).
 template <bool TA, bool TB, int EPI = bmb::EPI_BLAS>
-void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
+bool dispatch(int batch, int M, int N, int K, float alpha, const float *A,
               long long sA, const float *B, long long sB, float beta, float *C,
-              long long sC, hipStream_t stream, bmb::EpiArgs ep = {}) {
-    if (M <= 0 || N <= 0 || batch <= 0) return;
+              long long sC, hipStream_t stream, bmb::EpiArgs ep = {},
+              float *fixed = nullptr) {
+    if (M <= 0 || N <= 0 || batch <= 0) return true;
     // 128-bit loads need the contiguous axis of each stored operand to be a
     // multiple of 4 floats, 16-byte aligned bases, and batch strides that keep
     // that alignment.
@@ -240,22 +289,31 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && al16(A) && al16(B) &&
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
     const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
-    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
+    Plan p = fixed ? pick(M, N, K, batch, batch == 1, occ, NOALLOC_SPLIT_FLOATS)
+                   : pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
     float *P = nullptr;
     std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1) {
+    if (p.splits > 1 && fixed) {
+        if ((long long)p.splits * M * N > NOALLOC_SPLIT_FLOATS) {
+            fprintf(stderr, "gemm_noalloc: %d x %d x %d in %d K ranges needs %lld floats of "
+                    "partials, above the %lld of the fixed scratch array\n", M, N, K, p.splits,
+                    (long long)p.splits * M * N, NOALLOC_SPLIT_FLOATS);
+            return false;
+        }
+        P = fixed;
+    } else if (p.splits > 1) {
         lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
     }
     if (p.splits > 1) {
         switch (p.tile.kind) {
-        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
-        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
-        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
-        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep); break;
+        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
         }
-        return;
+        return true;
     }
     switch (p.tile.kind) {
     case TileKind::L:
@@ -271,15 +329,17 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
         launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     }
+    return true;
 }
 
-void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
+bool gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
               const float *A, long long sA, const float *B, long long sB,
-              float beta, float *C, long long sC, hipStream_t stream) {
-    if (!ta && !tb)     dispatch<false, false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
-    else if (!ta && tb) dispatch<false, true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
-    else if (ta && !tb) dispatch<true,  false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
-    else                dispatch<true,  true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
+              float beta, float *C, long long sC, hipStream_t stream, float *fixed = nullptr) {
+    const bmb::EpiArgs ep{};
+    if (!ta && !tb)     return dispatch<false, false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
+    else if (!ta && tb) return dispatch<false, true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
+    else if (ta && !tb) return dispatch<true,  false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
+    else                return dispatch<true,  true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
 }
 
 }  // namespace
@@ -319,6 +379,16 @@ void batched_gemm(bool transA, bool transB, int batch, int M, int N, int K,
 void sgemm_tensorcore(int M, int N, int K, float alpha, const float *A,
                       const float *B, float beta, float *C) {
     gemm_any(false, false, 1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, nullptr);
+}
+
+int gemm_noalloc(bool transA, bool transB, int M, int N, int K, float alpha, const float *A,
+                 const float *B, float beta, float *C, hipStream_t stream) {
+    if (M <= 0 || N <= 0) return 0;
+    float *fixed = noalloc_scratch();
+    if (fixed == nullptr) return -1;
+    return gemm_any(transA, transB, 1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, fixed)
+               ? 0
+               : -1;
 }
 
 }  // extern "C"

@@ -42,6 +42,25 @@ void batched_gemm(bool transA, bool transB, int batch, int M, int N, int K,
                   const float *B, long long strideB, float beta, float *C,
                   long long strideC, hipStream_t stream BMB_DEFAULT_STREAM);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc): gemm() that allocates nothing. Its split-K partial sums
+ * live in a fixed 64 MiB array of the library's device memory (one per GPU,
+ * held until the process ends) instead of leased scratch, so unlike gemm()
+ * it also splits K on non-null streams. The planner only considers splits
+ * whose partials (splits * M * N floats) fit the array; shapes that would
+ * need more run with fewer K ranges or none, so no size is refused for its
+ * scratch. The first call on a device resolves the array's address (do it
+ * once outside any graph capture). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, or host threads on
+ * different streams) race on it and must be ordered by the caller. Nothing
+ * in the array needs to start at zero (every partial is written before it
+ * is read). Returns 0 once the work is queued, -1 with a message on stderr
+ * if the array cannot be resolved or a plan would not fit it. */
+int gemm_noalloc(bool transA, bool transB, int M, int N, int K, float alpha,
+                 const float *A, const float *B, float beta, float *C,
+                 hipStream_t stream BMB_DEFAULT_STREAM);
+
 #pragma GCC visibility pop
 #ifdef __cplusplus
 }
