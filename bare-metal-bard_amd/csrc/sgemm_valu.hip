@@ -7,28 +7,36 @@
 // stages 1-7). Split-K, reassociation or MFMA would all break that, which is
 // why this stage stays on the vector ALU.
 //
-// Ceiling. This build never emits packed fp32 (v_pk_fma_f32). A single wave
-// issues one v_fmac_f32 every 4 clocks, but several waves on one SIMD issue
-// concurrently: a loop of nothing but FMAs reaches ~112 TFLOP/s (71% of the
-// 157.3 TFLOP/s vector peak) with 8 waves per SIMD, which is the practical
-// ceiling of a kernel that also has to read its operands from LDS.
+// Ceiling. This build never emits packed fp32 (v_pk_fma_f32). gfx950 issues
+// plain v_fmac_f32 from two waves of one SIMD at once (its second VALU port):
+// a loop of nothing but FMAs with 32 or more independent accumulators per lane
+// reaches 128-136 TFLOP/s (81-86% of the 157.3 TFLOP/s vector peak) with 2 to
+// 8 waves per SIMD, ~70 with one. A GEMM also reads its operands from LDS;
+// the counters of the 128 x 128 tile at N = 4096 show 94% of its VALU
+// instructions are FMAs, a third of them issued on the second port.
 //
 // Structure.
-//   * 256 lanes = 4 wave64 per workgroup, 128x128 output tile, BK = 16.
-//   * Each wave owns a 64x64 quadrant; each lane an 8x8 patch made of two
-//     4-row strips 32 rows apart and two 4-column strips 32 columns apart.
-//     The 8 lanes sharing a strip row read one float4 each of a 32-float
-//     LDS span, so every per-k LDS read is conflict-free and 128-bit.
+//   * 256 lanes = 4 wave64 per workgroup; tiles of 128 x 128, 64 x 128 and
+//     64 x 64 outputs, chosen per shape (pick_tile): the small tiles fill the
+//     device when M x N is small, the large one reads less LDS per FMA.
+//   * Each wave owns a quarter of the tile; each lane a patch of 4 x 4 strips
+//     (two 4-row strips 32 rows apart and two 4-column strips 32 columns
+//     apart in the 128 x 128 tile). The 8 lanes sharing a strip row read one
+//     float4 each of a 32-float LDS span, so every per-k LDS read is 128-bit.
 //   * A is stored k-major in LDS (As[k][m], +4 pad so the transposing
-//     stores spread over all banks); B is stored as it lies (Bs[k][n]).
-//   * Double-buffered LDS with the next tile prefetched into registers while
-//     the current one is consumed: one barrier per BK chunk.
+//     stores spread over the banks); B is stored as it lies (Bs[k][n]).
+//   * Double-buffered LDS with the next k-tile prefetched into registers while
+//     the current one is consumed: one barrier per k-tile.
 //   * Ragged M, N, K are handled in-kernel: guarded, zero-filled loads and
 //     guarded stores. There is no fallback kernel. VEC selects aligned 128-bit
 //     global access when K % 4 == 0, N % 4 == 0 and the pointers are 16-byte
 //     aligned; otherwise interior chunks still use dword-aligned 128-bit loads
 //     and only a chunk that straddles a row end uses 32-bit loads.
 //   * Workgroup ids are remapped so the tiles one XCD runs share panels.
+#include <math.h>
+
+#include <mutex>
+
 #include "common.hpp"
 #include "../../include/kernels.h"
 #include "launch.hpp"
@@ -38,27 +46,45 @@ using bmb::fma_rn;
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 16, NT = 256;
+constexpr int NT = 256;
 constexpr int APAD = 4;
-constexpr int LDA = BM + APAD;  // As row (one k) width
-constexpr int LDB = BN;         // Bs row width
 
-// Per-thread share of one tile: A is BM x BK = 2048 floats, B is BK x BN =
-// 2048 floats, i.e. 8 floats of each per lane.
-struct Prefetch {
-    float a[8];
-    float b[8];
+// Tile of 64*TMS x 64*TNS outputs for 4 waves (2 x 2), each wave a
+// 32*TMS x 32*TNS quadrant; each lane a patch of TMS x TNS strips of 4 x 4
+// outputs, strips 32 rows / columns apart, so the 8 lanes sharing a strip row
+// (or column) read one float4 each of a 32-float LDS span per k: every LDS
+// read is conflict-free and 128-bit. 128 x 128 (TMS = TNS = 2) keeps 64
+// accumulators per lane and reads 1 byte of LDS per FMA; 64 x 64 (1, 1) has 4x
+// the workgroups for a small C at 2 bytes per FMA.
+template <int TMS_, int TNS_, int BK_, int UNROLL_>
+struct ValuTile {
+    static constexpr int TMS = TMS_, TNS = TNS_;
+    static constexpr int BK = BK_;          // k per LDS stage
+    static constexpr int UNROLL = UNROLL_;  // k-loop unroll within a stage
+    static constexpr int BM = 64 * TMS, BN = 64 * TNS;
+    static constexpr int LDA = BM + APAD;  // As row (one k) width
+    static constexpr int LDB = BN;         // Bs row width
+    static constexpr int A_CH = BM * BK / 4 / NT;  // float4 chunks per lane
+    static constexpr int B_CH = BK * BN / 4 / NT;
+    static constexpr int KCH = BK / 4;             // float4 chunks per A row
 };
 
-template <bool VEC>
-__device__ __forceinline__ void load_tile(Prefetch &p, const float *A,
+// Per-thread share of one k-tile of A (BM x BK) and B (BK x BN).
+template <class Tl>
+struct Prefetch {
+    float a[4 * Tl::A_CH];
+    float b[4 * Tl::B_CH];
+};
+
+template <class Tl, bool VEC>
+__device__ __forceinline__ void load_tile(Prefetch<Tl> &p, const float *A,
                                           const float *B, int M, int N, int K,
                                           int cRow, int cCol, int k0, int tid) {
-    // A chunk e = tid + r*NT (r = 0,1): row m = e / 4, k offset (e % 4) * 4.
+    // A chunk e = tid + r*NT: row m = e / KCH, k offset (e % KCH) * 4.
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < Tl::A_CH; ++r) {
         const int e = tid + r * NT;
-        const int m = e >> 2, kc = (e & 3) * 4;
+        const int m = e / Tl::KCH, kc = (e % Tl::KCH) * 4;
         const int gm = cRow + m, gk = k0 + kc;
         if (VEC) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -77,11 +103,11 @@ __device__ __forceinline__ void load_tile(Prefetch &p, const float *A,
                 p.a[r * 4 + i] = (gm < M && gk + i < K) ? A[(size_t)gm * K + gk + i] : 0.0f;
         }
     }
-    // B chunk e: row k = e / 32, n offset (e % 32) * 4.
+    // B chunk e: row k = e / (BN/4), n offset (e % (BN/4)) * 4.
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < Tl::B_CH; ++r) {
         const int e = tid + r * NT;
-        const int k = e >> 5, nc = (e & 31) * 4;
+        const int k = e / (Tl::BN / 4), nc = (e % (Tl::BN / 4)) * 4;
         const int gk = k0 + k, gn = cCol + nc;
         if (VEC) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -101,96 +127,103 @@ __device__ __forceinline__ void load_tile(Prefetch &p, const float *A,
     }
 }
 
-__device__ __forceinline__ void store_tile(const Prefetch &p, float *As,
+template <class Tl>
+__device__ __forceinline__ void store_tile(const Prefetch<Tl> &p, float *As,
                                            float *Bs, int tid) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < Tl::A_CH; ++r) {
         const int e = tid + r * NT;
-        const int m = e >> 2, kc = (e & 3) * 4;
+        const int m = e / Tl::KCH, kc = (e % Tl::KCH) * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) As[(kc + i) * LDA + m] = p.a[r * 4 + i];
+        for (int i = 0; i < 4; ++i) As[(kc + i) * Tl::LDA + m] = p.a[r * 4 + i];
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < Tl::B_CH; ++r) {
         const int e = tid + r * NT;
-        const int k = e >> 5, nc = (e & 31) * 4;
-        bmb::st4(&Bs[k * LDB + nc],
+        const int k = e / (Tl::BN / 4), nc = (e % (Tl::BN / 4)) * 4;
+        bmb::st4(&Bs[k * Tl::LDB + nc],
                  make_float4(p.b[r * 4 + 0], p.b[r * 4 + 1], p.b[r * 4 + 2], p.b[r * 4 + 3]));
     }
 }
 
-template <bool VEC>
+template <class Tl, bool VEC>
 __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
                                                    float alpha,
                                                    const float *__restrict__ A,
                                                    const float *__restrict__ B,
                                                    float beta, float *C,
                                                    int tiles_m, int tiles_n) {
-    __shared__ float As[2][BK * LDA];
-    __shared__ float Bs[2][BK * LDB];
+    constexpr int TM = 4 * Tl::TMS, TN = 4 * Tl::TNS;  // outputs per lane
+    constexpr int BK = Tl::BK;
+    __shared__ float As[2][BK * Tl::LDA];
+    __shared__ float Bs[2][BK * Tl::LDB];
 
     const int nblocks = tiles_m * tiles_n;
     int tm, tn;
     bmb::group_tile(bmb::xcd_remap(blockIdx.x, nblocks), tiles_m, tiles_n, 8, tm, tn);
-    const int cRow = tm * BM, cCol = tn * BN;
+    const int cRow = tm * Tl::BM, cCol = tn * Tl::BN;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave >> 1) * (Tl::BM / 2), wn = (wave & 1) * (Tl::BN / 2);
     const int lr = lane >> 3, lc = lane & 7;
 
-    float acc[8][8];
+    float acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+        for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
 
     const int nkt = (K + BK - 1) / BK;
-    Prefetch pf;
+    Prefetch<Tl> pf;
     if (nkt > 0) {
-        load_tile<VEC>(pf, A, B, M, N, K, cRow, cCol, 0, tid);
-        store_tile(pf, As[0], Bs[0], tid);
+        load_tile<Tl, VEC>(pf, A, B, M, N, K, cRow, cCol, 0, tid);
+        store_tile<Tl>(pf, As[0], Bs[0], tid);
     }
     __syncthreads();
 
     for (int kt = 0; kt < nkt; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nkt;
-        if (more) load_tile<VEC>(pf, A, B, M, N, K, cRow, cCol, (kt + 1) * BK, tid);
+        if (more) load_tile<Tl, VEC>(pf, A, B, M, N, K, cRow, cCol, (kt + 1) * BK, tid);
 
         const float *as = As[cur] + wm + lr * 4;
         const float *bs = Bs[cur] + wn + lc * 4;
-        // Unrolled by 2 only: a full unroll lets the scheduler hoist all 16
-        // k-steps' LDS reads and pushes the lane past 256 VGPRs.
-#pragma unroll 2
+        // The 128 x 128 tile unrolls by 2 only: a full unroll lets the
+        // scheduler hoist all k-steps' LDS reads and pushes the lane past 256
+        // VGPRs. The small tiles (one wave per SIMD at small N) unroll fully,
+        // so the reads of later k-steps are in flight during the FMAs.
+#pragma unroll Tl::UNROLL
         for (int k = 0; k < BK; ++k) {
-            float ra[8], rb[8];
-            const float4 a0 = bmb::ld4(as + k * LDA);
-            const float4 a1 = bmb::ld4(as + k * LDA + 32);
-            const float4 b0 = bmb::ld4(bs + k * LDB);
-            const float4 b1 = bmb::ld4(bs + k * LDB + 32);
-            ra[0] = a0.x; ra[1] = a0.y; ra[2] = a0.z; ra[3] = a0.w;
-            ra[4] = a1.x; ra[5] = a1.y; ra[6] = a1.z; ra[7] = a1.w;
-            rb[0] = b0.x; rb[1] = b0.y; rb[2] = b0.z; rb[3] = b0.w;
-            rb[4] = b1.x; rb[5] = b1.y; rb[6] = b1.z; rb[7] = b1.w;
+            float ra[TM], rb[TN];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int s = 0; s < Tl::TMS; ++s) {
+                const float4 a = bmb::ld4(as + k * Tl::LDA + 32 * s);
+                ra[4 * s + 0] = a.x; ra[4 * s + 1] = a.y; ra[4 * s + 2] = a.z; ra[4 * s + 3] = a.w;
+            }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = fma_rn(ra[i], rb[j], acc[i][j]);
+            for (int s = 0; s < Tl::TNS; ++s) {
+                const float4 b = bmb::ld4(bs + k * Tl::LDB + 32 * s);
+                rb[4 * s + 0] = b.x; rb[4 * s + 1] = b.y; rb[4 * s + 2] = b.z; rb[4 * s + 3] = b.w;
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = fma_rn(ra[i], rb[j], acc[i][j]);
         }
 
-        if (more) store_tile(pf, As[cur ^ 1], Bs[cur ^ 1], tid);
+        if (more) store_tile<Tl>(pf, As[cur ^ 1], Bs[cur ^ 1], tid);
         __syncthreads();
     }
 
     // Epilogue. Row of acc[i][.]: wm + (i/4)*32 + lr*4 + i%4; column of
     // acc[.][h*4+x]: wn + h*32 + lc*4 + x.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < TM; ++i) {
         const int r = cRow + wm + (i >> 2) * 32 + lr * 4 + (i & 3);
         if (r >= M) continue;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < Tl::TNS; ++h) {
             const int c = cCol + wn + h * 32 + lc * 4;
             float *dst = C + (size_t)r * N + c;
             if (VEC && c + 3 < N) {
@@ -210,20 +243,106 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
     }
 }
 
+template <class Tl>
+void launch_valu(int M, int N, int K, float alpha, const float *A, const float *B, float beta,
+                 float *C, bool vec) {
+    const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
+    const dim3 grid(tiles_m * tiles_n);
+    if (vec)
+        bmb::launch(sgemm_valu_k<Tl, true>, grid, dim3(NT), 0, nullptr, M, N, K, alpha, A, B,
+                    beta, C, tiles_m, tiles_n);
+    else
+        bmb::launch(sgemm_valu_k<Tl, false>, grid, dim3(NT), 0, nullptr, M, N, K, alpha, A, B,
+                    beta, C, tiles_m, tiles_n);
+}
+
+// The tiles (bit-identical to one another: every one keeps each output's
+// sequential k order) and their measured throughput on MI355X when the device
+// is full of them (TFLOP/s at N = 8192).
+using TileL = ValuTile<2, 2, 16, 8>;  // 128 x 128: 88
+using TileW = ValuTile<1, 2, 16, 2>;  // 64 x 128: 84.5
+using TileS = ValuTile<1, 1, 32, 8>;  // 64 x 64: 78
+
+struct ValuCand {
+    int bm, bn;
+    double tflops;
+};
+constexpr ValuCand VCANDS[] = {{128, 128, 88.0}, {64, 128, 84.5}, {64, 64, 78.0}};
+
+template <class Tl>
+int valu_occupancy() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, sgemm_valu_k<Tl, true>, NT, 0) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        n = 1;
+    }
+    return n < 1 ? 1 : n;
+}
+
+// Tile choice: a tile's workgroups run in rounds of cus * occupancy; a last,
+// part-filled round runs each CU's workgroups faster (fewer share its SIMDs),
+// by (held / fit)^0.88 of a full round (the GEMM planner's fit). A larger tile
+// reads less LDS per FMA; a smaller one fills the device at small M x N (at
+// N = 1024: 64 workgroups of 128 x 128 for 256 CUs). Measured on the square
+// sweep: 64 x 64 up to N = 3072 (N = 1024: 37 instead of 11 TFLOP/s),
+// 64 x 128 at the ragged 4097, 128 x 128 from 4096.
+int pick_tile(int M, int N) {
+    static std::once_flag once[64];
+    static int occ[64][3], cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    std::call_once(once[dev], [&] {
+        occ[dev][0] = valu_occupancy<TileL>();
+        occ[dev][1] = valu_occupancy<TileW>();
+        occ[dev][2] = valu_occupancy<TileS>();
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            c <= 0) {
+            (void)hipGetLastError();
+            c = 256;
+        }
+        cus[dev] = c;
+    });
+    int best = 0;
+    double best_t = -1.0;
+    for (int t = 0; t < 3; ++t) {
+        const ValuCand &v = VCANDS[t];
+        const long long tiles = (long long)bmb::ceil_div(M, v.bm) * bmb::ceil_div(N, v.bn);
+        const long long slots = (long long)cus[dev] * occ[dev][t];
+        const double t_item = (double)v.bm * v.bn * occ[dev][t] / v.tflops;
+        const long long full = tiles / slots, rem = tiles % slots;
+        double time = full * t_item;
+        if (rem) {
+            const long long per_cu = (rem + cus[dev] - 1) / cus[dev];
+            time += per_cu < occ[dev][t] ? t_item * pow((double)per_cu / occ[dev][t], 0.88)
+                                         : t_item;
+        }
+        if (best_t < 0 || time < best_t) {
+            best_t = time;
+            best = t;
+        }
+    }
+    return best;
+}
+
+// tile: 0 = 128x128, 1 = 64x128, 2 = 64x64.
+void run_valu(int tile, int M, int N, int K, float alpha, const float *A, const float *B,
+              float beta, float *C) {
+    const bool vec = (K % 4 == 0) && (N % 4 == 0) && (((uintptr_t)A & 15) == 0) &&
+                     (((uintptr_t)B & 15) == 0) && (((uintptr_t)C & 15) == 0);
+    switch (tile) {
+    case 0: launch_valu<TileL>(M, N, K, alpha, A, B, beta, C, vec); break;
+    case 1: launch_valu<TileW>(M, N, K, alpha, A, B, beta, C, vec); break;
+    default: launch_valu<TileS>(M, N, K, alpha, A, B, beta, C, vec); break;
+    }
+}
+
 }  // namespace
 
 extern "C" void sgemm_doublebuffer(int M, int N, int K, float alpha,
                                    const float *A, const float *B, float beta,
                                    float *C) {
     if (M <= 0 || N <= 0) return;
-    const int tiles_m = bmb::ceil_div(M, BM), tiles_n = bmb::ceil_div(N, BN);
-    const bool vec = (K % 4 == 0) && (N % 4 == 0) && (((uintptr_t)A & 15) == 0) &&
-                     (((uintptr_t)B & 15) == 0) && (((uintptr_t)C & 15) == 0);
-    const dim3 grid(tiles_m * tiles_n);
-    if (vec)
-        bmb::launch(sgemm_valu_k<true>, grid, dim3(NT), 0, nullptr, M, N, K,
-                    alpha, A, B, beta, C, tiles_m, tiles_n);
-    else
-        bmb::launch(sgemm_valu_k<false>, grid, dim3(NT), 0, nullptr, M, N, K,
-                    alpha, A, B, beta, C, tiles_m, tiles_n);
+    run_valu(pick_tile(M, N), M, N, K, alpha, A, B, beta, C);
 }

@@ -46,6 +46,9 @@ sys.path.insert(0, os.path.join(ROOT, "bare-metal-bard_amd"))
 
 PEAK_FP32_TFLOPS = 157.3     # MI355X fp32 vector = fp32 matrix (published)
 PEAK_BF16_TFLOPS = 2500.0    # dense bf16 MFMA (published)
+# KERNELS id 10 issues three bf16 MFMAs per fp32 product term, so its own
+# ceiling is a third of the bf16 peak in fp32-equivalent flops.
+BF16X3_CEILING_TFLOPS = PEAK_BF16_TFLOPS / 3
 PEAK_HBM_GBS = 8000.0
 N_SGEMM = 4096
 SWEEP_N = (512, 1000, 1024, 1536, 2048, 4096, 4097, 6144, 8192)
@@ -59,14 +62,17 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--kernel", type=int, default=9, help="headline KERNELS id")
+    ap.add_argument("--n", type=int, default=N_SGEMM,
+                    help="size of the headline SGEMM (M=N=K; for profiling other sizes)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-telemetry", action="store_true",
                     help="skip the untimed sustained runs that read clock and power (for "
                          "profiling runs, whose per-step kernel totals they would inflate)")
     ap.add_argument("--no-ladder", action="store_true", help="skip the ladder, sweep and GPT shapes")
     ap.add_argument("--quick", action="store_true", help="headline SGEMM and flash only")
-    ap.add_argument("--only", choices=["sgemm", "flash", "gpt"], default=None,
-                    help="run one workload only (for profiling)")
+    ap.add_argument("--only", choices=["sgemm", "flash", "gpt", "sizes"], default=None,
+                    help="run one workload only (for profiling); sizes: KERNELS ids 8, 9 "
+                         "and 10 at N = 512, 1024 and 4096")
     ap.add_argument("--flash-sweep", action="store_true",
                     help="also time every forward and backward flash config (as the "
                          "reference's tools/test_flash.cu:198-227,279-319 sweep does)")
@@ -282,6 +288,25 @@ def load_traffic():
         return json.load(f)
 
 
+def cpu_model():
+    """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def own_peak(kid):
+    """(peak TFLOP/s, its name) a KERNELS id is measured against."""
+    if kid == 10:
+        return BF16X3_CEILING_TFLOPS, "bf16x3 ceiling = bf16 dense peak / 3"
+    return PEAK_FP32_TFLOPS, "fp32 peak (vector = matrix)"
+
+
 def host_threads():
     n = len(os.sched_getaffinity(0))
     return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
@@ -308,6 +333,7 @@ def cpu_sgemm_baseline(O, A, B, C0, N):
                   threads=1)
     dt1 = time.perf_counter() - t0
     return {"value": round(gf, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "cpus_online": os.cpu_count(),
             "sample": "sequential-fmaf SGEMM (oracle orc_gemm_f32seq_mt, bit-identical to "
                       "KERNELS ids 1-8), rows 0-%d of the N=4096 alpha=1 beta=0.5 problem, "
                       "%.1f s" % (rows - 1, dt),
@@ -335,6 +361,7 @@ def cpu_flash_baseline(O, qkv, dout, B, T, C, NH):
     pairs = done * NH * T * (T + 1) / 2
     tf = 14.0 * hs * pairs / dt / 1e12  # fwd 4*d*P + bwd 10*d*P useful flops
     return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "cpus_online": os.cpu_count(),
             "sample": "unfused fp32 attention fwd+bwd (oracle orc_attn_fwdbwd_f32), batches "
                       "0-%d of 8 (12 heads, T=1024, d=64), %.1f s" % (done - 1, dt)}
 
@@ -384,12 +411,12 @@ def main():
             "data": "synthetic (xorshift32 1e-3 grid inputs with the seeds of "
                     "src/bench.cu:226-228; attention q,k,v,dO N(0,1) by Box-Muller)"}
 
-    N = N_SGEMM
+    N = args.n
     A = O.fill_xorshift(N * N, 0x12345678).reshape(N, N)
     Bm = O.fill_xorshift(N * N, 0x9ABCDEF0).reshape(N, N)
     C0 = O.fill_xorshift(N * N, 0x0F0F0F0F).reshape(N, N)
     if args.only in (None, "sgemm"):
-        smax = max(SWEEP_N) if extras else N
+        smax = max(max(SWEEP_N), N) if extras else N
         dA = torch.from_numpy(O.fill_xorshift(smax * smax, 0x12345678)).cuda()
         dB = torch.from_numpy(O.fill_xorshift(smax * smax, 0x9ABCDEF0)).cuda()
         dC = torch.from_numpy(O.fill_xorshift(smax * smax, 0x0F0F0F0F)).cuda()
@@ -411,18 +438,20 @@ def main():
         line.update({
             "value": round(g, 1), "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
             "pct_of_peak": round(100 * g / 1e3 / PEAK_FP32_TFLOPS, 1),
-            "config": {"workload": "sgemm M=N=K=4096 fp32 row-major alpha=1 beta=0.5, "
-                                   "KERNELS id %d (%s)" % (args.kernel, ent["name"]),
+            "config": {"workload": "sgemm M=N=K=%d fp32 row-major alpha=1 beta=0.5, "
+                                   "KERNELS id %d (%s)" % (N, args.kernel, ent["name"]),
                        "tol": ent["tol"], "algorithmic_gflop": round(flops / 1e9, 2),
                        "algorithmic_mb": round(bytes_alg / 1e6, 1)},
-            "roofline": {"bound": "mfma", "achieved": round(g / 1e3, 2),
-                         "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(g / 1e3 / PEAK_FP32_TFLOPS, 4),
-                         "traffic": traffic.get("sgemm_id%d_4096" % args.kernel)},
+            "roofline": {"bound": "mfma" if args.kernel >= 9 else "valu",
+                         "achieved": round(g / 1e3, 2),
+                         "peak": own_peak(args.kernel)[0], "unit": "TFLOP/s",
+                         "frac": round(g / 1e3 / own_peak(args.kernel)[0], 4),
+                         "peak_is": own_peak(args.kernel)[1],
+                         "traffic": traffic.get("sgemm_id%d_%d" % (args.kernel, N))},
             "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
             "independent_runs": independent_runs(sq(args.kernel, N), args.steps, ms),
             "warmup_steps_run": WARM_STEPS_RUN.get("sgemm"),
-            "vendor_fp32_gemm_gflops": vendor_sq(torch, dA, dB, dC, N),
+            "vendor_fp32_gemm_gflops": vendor_sq(torch, dA, dB, dC, N) if extras else None,
             "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
         })
 
@@ -433,6 +462,10 @@ def main():
                 ms1 = timed_burst(sq(kid, 1024, 1.0, 0.0), 20, 5)
                 c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3, ms1)
             line["config1_n1024_gflops"] = c1
+            line["id10_denominator"] = {
+                "bf16x3_ceiling_tflops": round(BF16X3_CEILING_TFLOPS, 1),
+                "why": "three bf16 MFMAs per fp32 product term (hi*hi + hi*lo + lo*hi); id 10's "
+                       "pct figures below are of this ceiling, ids 1-9 of the 157.3 fp32 peak"}
             # Config 2: square sweep, alpha=1, beta=0.5.
             sweep = {}
             for kid in (8, 9, 10):
@@ -448,16 +481,19 @@ def main():
             for kid in range(1, 11):
                 reps, warm = (2, 1) if kid <= 2 else (5, 2)
                 s3 = stats(timed(sq(kid, N), reps, warm))
+                pk, pk_name = own_peak(kid)
                 ladder["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = {
                     "gflops": gf(flops, s3["median_ms"]),
-                    "pct_fp32_peak": round(100 * flops / s3["median_ms"] / 1e9
-                                           / PEAK_FP32_TFLOPS, 1)}
+                    "pct_of_own_peak": round(100 * flops / s3["median_ms"] / 1e9 / pk, 1),
+                    "peak_tflops": round(pk, 1)}
             bmb.check("ladder")
-            line["ladder_n4096"] = ladder
+            line["ladder_n%d" % N] = ladder
             del dA, dB, dC
             torch.cuda.empty_cache()
             line["config3_gpt_gemm_gflops"] = gpt_shapes(bmb, O, torch)
 
+    if args.only == "sizes":
+        line["sgemm_sizes_gflops"] = sizes_bench(bmb, O, torch)
     if args.only in (None, "flash"):
         line["flash"] = flash_bench(args, bmb, O, torch, traffic)
     if args.only == "gpt" or (args.only is None and not args.quick):
@@ -478,6 +514,26 @@ def main():
                 cpu = fl
         line["cpu_baseline"] = cpu
     print(json.dumps(line))
+
+
+def sizes_bench(bmb, O, torch):
+    """KERNELS ids 8 (fp32 VALU), 9 (fp32 MFMA) and 10 (bf16x3) at N = 512,
+    1024 and 4096 with config 2's epilogue (alpha 1, beta 0.5, C pre-filled),
+    a burst of launches each: the workload of the rocprofv3 counter runs for
+    the VALU and bf16x3 paths and for the small shapes, whose few output
+    tiles leave most CUs idle."""
+    res = {}
+    for n in (512, 1024, 4096):
+        dA = torch.from_numpy(O.fill_xorshift(n * n, 0x12345678)).cuda()
+        dB = torch.from_numpy(O.fill_xorshift(n * n, 0x9ABCDEF0)).cuda()
+        dC = torch.from_numpy(O.fill_xorshift(n * n, 0x0F0F0F0F)).cuda()
+        for kid in (8, 9, 10):
+            fn = sgemm_fn(bmb, kid)
+            run = lambda: fn(n, n, n, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr())
+            res["id%d N=%d" % (kid, n)] = gf(2.0 * n ** 3, timed_burst(run, 10 if n > 1024 else 50))
+        bmb.check("sgemm sizes")
+        del dA, dB, dC
+    return res
 
 
 def vendor_sq(torch, dA, dB, dC, N):
