@@ -360,6 +360,12 @@ void bmb::gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B,
                                                bmb::EpiArgs{nullptr, nullptr, pre});
 }
 
+void bmb::splitk_reduce(float *C, const float *P, int splits, long long mn, int N, float alpha,
+                        float beta, hipStream_t stream) {
+    bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BLAS>, dim3((unsigned)((mn + 1023) / 1024)),
+                dim3(256), 0, stream, C, P, splits, mn, N, alpha, beta, bmb::EpiArgs{});
+}
+
 extern "C" {
 
 void gemm(bool transA, bool transB, int M, int N, int K, float alpha,
