@@ -1,8 +1,11 @@
 // Fused causal attention, forward and backward, for gfx950 -- the
 // counterpart of bare-metal-bard's src/flash.cu (API: src/flash.h).
 //
-// Every contraction is a chain of v_mfma_f32_32x32x2_f32 (fp32 in, exact fp32
-// products, fp32 accumulate). In that instruction lane l supplies
+// The default forward (flash_fwd_h_k, below) carries every fp32 operand as an
+// fp16 hi/lo pair on v_mfma_f32_32x32x16_f16 with exact power-of-two scaling;
+// its comment block gives the error and range argument. The other kernels use
+// chains of v_mfma_f32_32x32x2_f32 (fp32 in, exact fp32 products, fp32
+// accumulate). In that instruction lane l supplies
 // A[m = l%32][kk = l/32] and B[kk = l/32][n = l%32]; the 32x32 result leaves
 // lane l holding column n = l%32, register r holding row
 // res_row(r, l/32) = 8*(r/4) + 4*(l/32) + r%4. A 32-wide contraction over
@@ -460,6 +463,483 @@ flash_fwd_k(float *__restrict__ out, float *__restrict__ lse, const float *__res
                 bmb::st4(dst + d * 32 + 8 * r4 + 4 * hf,
                          make_float4(o[d][4 * r4 + 0] * inv, o[d][4 * r4 + 1] * inv,
                                      o[d][4 * r4 + 2] * inv, o[d][4 * r4 + 3] * inv));
+        if (hf == 0) lse[(size_t)bh * T + qi] = m * LN2 + logf(l);
+    }
+}
+
+// ------------------------------------------------------- forward, fp16x3
+//
+// The same online-softmax forward with every contraction on
+// v_mfma_f32_32x32x16_f16, whose fp16 products are exact in its fp32
+// accumulator. Each fp32 operand x is carried as two fp16 values,
+// hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32), and a product
+// a*b is accumulated as ah*bh + ah*bl + al*bh: what is dropped is al*bl and
+// the rounding of lo, each within 2^-22 |a b|, so a score or output element
+// carries about the error of an fp32 dot product (the fp32-MFMA forward above
+// rounds only its accumulation). That is 16 fp32 products per lane in 3
+// instructions of 32 cycles instead of 8 instructions of 64.
+//
+// Range. fp16 holds magnitudes up to 65504 and keeps 11 significant bits only
+// down to 2^-14, so nothing is converted unscaled: each query row, and each
+// 32-key tile of K and of V, is multiplied by a power of two 2^(14 - e), e the
+// binary exponent of its largest magnitude, which puts that magnitude in
+// [2^13, 2^14). Powers of two are exact and are undone exactly: a score is
+// s' * 2^(eq - 14) * 2^(ek - 14), one factor per lane and tile that rides on
+// the exp2 fma. For P V the tile factor of V moves onto P relative to the
+// largest V exponent E the wave has seen: P'' = P * 2^(ev - E + 7). P itself
+// may reach 2^8 (below), so P'' stays under 2^15, and when E grows the
+// accumulated O is rescaled by 2^(E_old - E_new). Any finite fp32 input range
+// works; within a tile, values far below the tile's largest lose digits only
+// below 2^-36 of it.
+//
+// Softmax. The running max m is only moved when a query's tile max exceeds it
+// by more than 8 (log2 units) or E grows -- a wave-uniform decision -- so the
+// O rescale is skipped on almost every tile; the probabilities exp2(s - m) of
+// the other tiles are then at most 2^8, and l and O carry the same stale m.
+//
+// Staging. The workgroup splits each K/V tile once into fp16 hi/lo planes in
+// LDS. The tile exponents need a maximum over the whole workgroup's loads, so
+// tile X is loaded into registers during tile X-3, its per-wave maxima are
+// published in LDS at the end of tile X-2, and it is split into the third of
+// three LDS buffers at the start of tile X-1: one barrier per tile, and more
+// than a tile's work between each load and its first use.
+//
+// Register layout. For 32x32x16 lane l supplies A[m = l%32][k = 8*(l/32)+i]
+// and B[k = 8*(l/32)+i][n = l%32], i = 0..7 (8 fp16 = 4 VGPRs), and gets the
+// result as in 32x32x2 (res_row). The score tile is again S^T = K Q^T; step st
+// of the head-dim contraction pairs lane half hf with dims hf*HS/2 + 8*st + i,
+// so a lane's query operand is HS/2 contiguous dims, as in the fp32 forward.
+// P^T then needs no data movement: registers 8*ks .. 8*ks+7 of a lane hold
+// keys 16*ks + {0..3, 8..11} (half 0) or 16*ks + {4..7, 12..15} (half 1), and
+// that set is the k index of step ks of O^T += V^T P^T; V^T rows in LDS store
+// each 16-key group in the order 0-3, 8-11, 4-7, 12-15 so that those 8 keys
+// are one 128-bit read.
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma_h(h8 a, h8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// x minus the fp16 value in half HIGH of the packed word h, in one
+// v_fma_mix_f32 (fp16 operand read directly; exact, as x - fp16(x) is
+// representable).
+template <bool HIGH>
+__device__ __forceinline__ float minus_half(unsigned h, float x) {
+    float r;
+    if (HIGH)
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(r) : "v"(h), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+
+// (a, b) -> hi = (fp16(a), fp16(b)), lo = (fp16(a - hi.a), fp16(b - hi.b)),
+// each pair packed in one 32-bit word (round to nearest even).
+__device__ __forceinline__ void split2(float a, float b, unsigned &hi, unsigned &lo) {
+    hi = __builtin_bit_cast(unsigned, __builtin_convertvector((f2v){a, b}, h2v));
+    const f2v r = {minus_half<false>(hi, a), minus_half<true>(hi, b)};
+    lo = __builtin_bit_cast(unsigned, __builtin_convertvector(r, h2v));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+// Max over the wave of a non-negative float (compared as integers, which
+// orders non-negative floats): DPP quad, half-row and row reductions, then the
+// four row results.
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+    int v = __float_as_int(x);
+    v = max(v, dpp_i<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = max(v, dpp_i<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = max(v, dpp_i<0x141>(v));  // row_half_mirror
+    v = max(v, dpp_i<0x140>(v));  // row_mirror
+    const int m = max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+                      max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+    return __int_as_float(m);
+}
+
+__device__ __forceinline__ float absmax4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Binary exponent e of a maximum m > 0 (2^(e-1) <= m < 2^e); NOEXP for m = 0.
+constexpr int NOEXP = -1000;
+__device__ __forceinline__ int max_exp(float m) {
+    return m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : NOEXP;
+}
+
+__device__ __forceinline__ int pair_max_i(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return max((int)r[0], (int)r[1]);
+}
+
+constexpr float SOFTMAX_SLACK = 8.0f;  // log2 units a stale running max may lag
+
+template <int HS>
+struct FwdSmemH {
+    static constexpr int LDK = HS + 8;  // halves per K row (+16 bytes)
+    static constexpr int LDV = 32 + 8;  // halves per V^T row (+16 bytes)
+    static constexpr int KPLANE = 32 * LDK * 2;  // bytes
+    static constexpr int VPLANE = HS * LDV * 2;
+    static constexpr int OFF_KL = KPLANE, OFF_VH = 2 * KPLANE, OFF_VL = 2 * KPLANE + VPLANE;
+    static constexpr int OFF_EXP = 2 * KPLANE + 2 * VPLANE;  // int2 (ek, ev) of the tile
+    static constexpr int BUF = OFF_EXP + 16;
+    static constexpr int NBUF = 3;
+    static constexpr size_t SLOTS = NBUF * (size_t)BUF;  // 2 x (2 x waves) floats follow
+    static size_t bytes(int waves) { return SLOTS + 2 * 2 * waves * sizeof(float); }
+};
+
+// Half-index of key kk (0..31) in V^T row d: 16-key groups in the order 0-3,
+// 8-11, 4-7, 12-15, and the four 16-byte chunks of the row XOR-swizzled by
+// d/16, so that the 32-bit stores of the rows d, d+16, d+32, d+48 from one
+// store phase fall in different banks.
+__device__ __forceinline__ int vt_pos(int d, int kk) {
+    const int p = (kk & 16) | (((kk >> 2) & 1) << 3) | (((kk >> 3) & 1) << 2) | (kk & 3);
+    return p ^ (((d >> 4) & 3) << 3);
+}
+
+// A 32-key tile of K and V for the fp16x3 forward in flight from global memory
+// to LDS. Thread tid holds float4 column c = tid % G (G = HS/4 lanes per row) of
+// keys 2p and 2p+1 of K and of V, p = tid / G + pass * (NT / G). Rows past
+// nrows re-read row nrows-1.
+template <int HS, int NT>
+struct KVTileH {
+    static constexpr int G = HS / 4;
+    static constexpr int PAIRS = NT / G;
+    static constexpr int PASSES = (16 + PAIRS - 1) / PAIRS;
+    static constexpr int NW = NT / 64;
+    float4 k[PASSES][2], v[PASSES][2];
+
+    __device__ __forceinline__ static bool has(int p) { return PAIRS * PASSES <= 16 || p < 16; }
+
+    __device__ __forceinline__ void load(const float *kb, const float *vb, size_t rs, int nrows,
+                                         int tid) {
+        const unsigned urs = (unsigned)rs;
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (!has(p)) {
+                    k[ps][j] = v[ps][j] = zero4();
+                    continue;
+                }
+                const unsigned o = 4u * ((unsigned)min(2 * p + j, nrows - 1) * urs + c);
+                k[ps][j] = ld4_at(kb, o);
+                v[ps][j] = ld4_at(vb, o);
+            }
+        }
+    }
+
+    // Publish this wave's max |K| and max |V| in slot[wave] and
+    // slot[NW + wave] (every lane stores the same uniform value). Rows past
+    // the end repeat row nrows-1, so they do not change the maxima; their
+    // keys are masked (probability 0), so they need no zeroing either.
+    __device__ __forceinline__ void publish(float *slot, int tid) const {
+        float ak = 0.0f, av = 0.0f;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                ak = fmaxf(ak, absmax4(k[ps][j]));
+                av = fmaxf(av, absmax4(v[ps][j]));
+            }
+        ak = wave_max_nonneg(ak);
+        av = wave_max_nonneg(av);
+        slot[tid >> 6] = ak;
+        slot[NW + (tid >> 6)] = av;
+    }
+
+    // Scale by the tile's powers of two, split and store (slot: the published
+    // maxima of this tile).
+    __device__ __forceinline__ void store(char *buf, const float *slot, int tid) const {
+        using S = FwdSmemH<HS>;
+        float mk = slot[0], mv = slot[NW];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mk = fmaxf(mk, slot[w]);
+            mv = fmaxf(mv, slot[NW + w]);
+        }
+        const int ek = max_exp(mk), ev = max_exp(mv);
+        const int sk = ek == NOEXP ? 0 : 14 - ek, sv = ev == NOEXP ? 0 : 14 - ev;
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+            if (!has(p)) continue;
+            float4 vs[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float4 kx = k[ps][j], vx = v[ps][j];
+                uint2 hi, lo;
+                split2(ldexpf(kx.x, sk), ldexpf(kx.y, sk), hi.x, lo.x);
+                split2(ldexpf(kx.z, sk), ldexpf(kx.w, sk), hi.y, lo.y);
+                // K row 2p+j, dims c..c+3: one 64-bit store per plane.
+                const int ko = (2 * p + j) * S::LDK * 2 + c * 2;
+                *reinterpret_cast<uint2 *>(buf + ko) = hi;
+                *reinterpret_cast<uint2 *>(buf + S::OFF_KL + ko) = lo;
+                vs[j] = make_float4(ldexpf(vx.x, sv), ldexpf(vx.y, sv), ldexpf(vx.z, sv),
+                                    ldexpf(vx.w, sv));
+            }
+            // V^T rows c..c+3, keys 2p and 2p+1 (adjacent positions): one
+            // 32-bit store per row and plane.
+            const float a0[4] = {vs[0].x, vs[0].y, vs[0].z, vs[0].w};
+            const float a1[4] = {vs[1].x, vs[1].y, vs[1].z, vs[1].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                unsigned hi, lo;
+                split2(a0[i], a1[i], hi, lo);
+                const int vo = ((c + i) * S::LDV + vt_pos(c + i, 2 * p)) * 2;
+                *reinterpret_cast<unsigned *>(buf + S::OFF_VH + vo) = hi;
+                *reinterpret_cast<unsigned *>(buf + S::OFF_VL + vo) = lo;
+            }
+        }
+        // Every thread stores the same (uniform) pair.
+        *reinterpret_cast<int2 *>(buf + S::OFF_EXP) = make_int2(ek, ev);
+    }
+};
+
+// One 32-key tile for this wave's 32 queries (see above). side1 and side2 are
+// the workgroup's staging work for later tiles, placed after the score and
+// after the P V MFMAs are issued so that their VALU work runs while the
+// matrix cores are busy.
+template <int HS, bool MASK, typename Side1, typename Side2>
+__device__ __forceinline__ void fwd_tile_h(const char *buf, const h8 (&qh)[HS / 16],
+                                           const h8 (&ql)[HS / 16], float fq,
+                                           f32x16 (&o)[HS / 32], float &m, float &l, int &E,
+                                           int kb, int qi, int T, int l32, int hf,
+                                           Side1 &&side1, Side2 &&side2) {
+    constexpr int NS = HS / 16, DT = HS / 32;
+    using S = FwdSmemH<HS>;
+    f32x16 s = zero16();
+    const char *kh = buf + l32 * S::LDK * 2 + hf * HS;  // dims hf*HS/2 .. (bytes)
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        const h8 ah = *reinterpret_cast<const h8 *>(kh + 16 * st);
+        const h8 al = *reinterpret_cast<const h8 *>(kh + S::OFF_KL + 16 * st);
+        s = mfma_h(ah, qh[st], s);
+        s = mfma_h(ah, ql[st], s);
+        s = mfma_h(al, qh[st], s);
+    }
+    side1();
+    const int2 ex = *reinterpret_cast<const int2 *>(buf + S::OFF_EXP);
+    const int ek = __builtin_amdgcn_readfirstlane(ex.x), ev = __builtin_amdgcn_readfirstlane(ex.y);
+    // Score = s' * fq * 2^(ek - 14); kept > 0 so that a masked -inf stays -inf.
+    const float fqk = fmaxf(ldexpf(fq, ek == NOEXP ? 0 : ek - 14), 1.17549435e-38f);
+    if (MASK) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kb + res_row(r, hf);
+            s[r] = ((key > qi) | (key >= T)) ? -INFINITY : s[r];
+        }
+    }
+    float mb = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+    const float mt = pair_max(mb) * fqk;  // finite: key 0 of the tile is live for every query
+    if (__builtin_amdgcn_ballot_w64(mt > m + SOFTMAX_SLACK) != 0 || ev > E) {
+        const float mn = fmaxf(m, mt);
+        const int En = max(E, ev);
+        const float alpha = exp2_hw(m - mn);  // 0 on the first tile
+        const float ao = ldexpf(alpha, E - En);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[d][r] *= ao;
+        l *= alpha;
+        m = mn;
+        E = En;
+    }
+    // P'' = exp2(score - m) * 2^g, g = ev - E + 7 <= 7.
+    const int g = ev - E + 7;
+    float pv[16], ls = 0.0f;
+    if (g >= -80) {
+        // 2^g folded into the exponent; l gets the sum back at scale 2^-g
+        // (every exp2(score - m) above 2^-40 is still a normal float here).
+        const float cm = m - (float)g;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pv[r] = exp2_hw(fmaf(s[r], fqk, -cm));
+            ls += pv[r];
+        }
+        l += ldexpf(ls, -g);
+    } else {
+        // A tile of V far below the largest seen (or all zero).
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = exp2_hw(fmaf(s[r], fqk, -m));
+            ls += p;
+            pv[r] = ldexpf(p, g);
+        }
+        l += ls;
+    }
+
+    h8 ph[2], pl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        unsigned hw[4], lw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            split2(pv[8 * ks + 2 * u], pv[8 * ks + 2 * u + 1], hw[u], lw[u]);
+        ph[ks] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+        pl[ks] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+    }
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+        const int row = d * 32 + l32;
+        const char *vr = buf + S::OFF_VH + row * S::LDV * 2;
+        const int sw = ((row >> 4) & 3) << 4;  // chunk swizzle of vt_pos, in bytes
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int off = (32 * ks + 16 * hf) ^ sw;
+            const h8 ah = *reinterpret_cast<const h8 *>(vr + off);
+            const h8 al = *reinterpret_cast<const h8 *>(vr + (S::OFF_VL - S::OFF_VH) + off);
+            o[d] = mfma_h(ah, ph[ks], o[d]);
+            o[d] = mfma_h(ah, pl[ks], o[d]);
+            o[d] = mfma_h(al, ph[ks], o[d]);
+        }
+    }
+    side2();
+}
+
+template <int HS, int WPB, int MINW>
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
+flash_fwd_h_k(float *__restrict__ out, float *__restrict__ lse, const float *__restrict__ qkv,
+              int T, int NH, int BH, float qscale, int cus, const unsigned *__restrict__ order) {
+    constexpr int NT = WPB * 64, QB = 32 * WPB, HH = HS / 2, NS = HS / 16, DT = HS / 32;
+    using S = FwdSmemH<HS>;
+    extern __shared__ float smem[];
+    char *sm = reinterpret_cast<char *>(smem);
+    float *slots = reinterpret_cast<float *>(sm + S::SLOTS);  // 2 x (2 x WPB)
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int nqb = (T + QB - 1) / QB;
+    int qb, bh;
+    if (order != nullptr) {
+        const unsigned e = order[blockIdx.x];
+        qb = (int)(e & 0xffffu);
+        bh = (int)(e >> 16);
+    } else {
+        work_item<true>(blockIdx.x, BH, nqb, true, cus, qb, bh);
+    }
+    const int b = bh / NH, h = bh % NH, C = NH * HS;
+    const size_t rs = 3 * (size_t)C;
+    const float *base = qkv + (size_t)b * T * rs + h * HS;
+
+    const int q0w = qb * QB + wave * 32;
+    const int qi = q0w + l32;
+    const bool active = q0w < T;
+
+    // Query operand: dims hf*HH .. hf*HH+HH-1 of query qi, times qscale, scaled
+    // by the query's power of two and split.
+    h8 qh[NS], ql[NS];
+    float fq;
+    {
+        float qv[HH];
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HH; j += 4) {
+            const float4 v = qi < T ? bmb::ld4(base + (size_t)qi * rs + hf * HH + j) : zero4();
+            qv[j + 0] = v.x * qscale; qv[j + 1] = v.y * qscale;
+            qv[j + 2] = v.z * qscale; qv[j + 3] = v.w * qscale;
+            amax = fmaxf(amax, absmax4(make_float4(qv[j], qv[j + 1], qv[j + 2], qv[j + 3])));
+        }
+        const int eq = max_exp(pair_max(amax));
+        fq = eq == NOEXP ? 1.0f : ldexpf(1.0f, eq - 14);  // > 0: masked scores stay -inf
+        const int sq = eq == NOEXP ? 0 : 14 - eq;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            unsigned hw[4], lw[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                split2(ldexpf(qv[8 * st + 2 * u], sq), ldexpf(qv[8 * st + 2 * u + 1], sq), hw[u],
+                       lw[u]);
+            qh[st] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+            ql[st] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+        }
+    }
+
+    f32x16 o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = zero16();
+    float m = -INFINITY, l = 0.0f;
+    int E = -200;  // below every finite fp32 exponent
+
+    const int kend = min(T, qb * QB + QB);
+    const int nkt = (kend + 31) / 32;
+    const int my_nkt = active ? (min(T, q0w + 32) + 31) / 32 : 0;
+    // Tile tt (clamped to the last one) of K and V.
+    auto load_tile = [&](KVTileH<HS, NT> &kv, int tt) {
+        const int kn = min(tt, nkt - 1) * 32;
+        kv.load(base + (size_t)kn * rs + C, base + (size_t)kn * rs + 2 * C, rs, min(32, T - kn),
+                tid);
+    };
+
+    // Tile X is loaded during tile X-3, its maxima published during X-2,
+    // split into LDS at the start of X-1: two register sets in flight.
+    KVTileH<HS, NT> ka, kb2;
+    load_tile(ka, 0);
+    load_tile(kb2, 1);
+    ka.publish(slots, tid);
+    __syncthreads();
+    ka.store(sm, slots, tid);
+    load_tile(ka, 2);
+    kb2.publish(slots + 2 * WPB, tid);
+    __syncthreads();
+
+    // cur holds tile t+1 (split now, then reloaded with tile t+3); nxt holds
+    // tile t+2 (maxima published after this tile's work).
+    auto step = [&](int t, KVTileH<HS, NT> &cur, KVTileH<HS, NT> &nxt) {
+        const int kb = t * 32;
+        // Split tile t+1 and reload its registers with tile t+3; publish the
+        // maxima of tile t+2.
+        // (Past the last tile these repeat it into buffers nobody reads.)
+        auto side1 = [&]() {
+            cur.store(sm + ((t + 1) % 3) * S::BUF, slots + ((t + 1) & 1) * 2 * WPB, tid);
+            load_tile(cur, t + 3);
+        };
+        auto side2 = [&]() { nxt.publish(slots + (t & 1) * 2 * WPB, tid); };
+        const char *buf = sm + (t % 3) * S::BUF;
+        if (t >= my_nkt) {
+            side1();
+            side2();
+        } else if (kb + 32 > q0w || kb + 32 > T) {
+            fwd_tile_h<HS, true>(buf, qh, ql, fq, o, m, l, E, kb, qi, T, l32, hf, side1, side2);
+        } else {
+            fwd_tile_h<HS, false>(buf, qh, ql, fq, o, m, l, E, kb, qi, T, l32, hf, side1, side2);
+        }
+        __syncthreads();
+    };
+    for (int t = 0; t < nkt; t += 2) {
+        step(t, kb2, ka);
+        if (t + 1 < nkt) step(t + 1, ka, kb2);
+    }
+
+    l = pair_sum(l);
+    if (active && qi < T) {
+        // O = O'' * 2^(E - 21) / l: the factors 2^(14 - ev) and 2^(ev - E + 7)
+        // carried by the V and P operands.
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const int es = E - 21;
+        float *dst = out + ((size_t)b * T + qi) * C + h * HS;
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                bmb::st4(dst + d * 32 + 8 * r4 + 4 * hf,
+                         make_float4(ldexpf(o[d][4 * r4 + 0] * inv, es),
+                                     ldexpf(o[d][4 * r4 + 1] * inv, es),
+                                     ldexpf(o[d][4 * r4 + 2] * inv, es),
+                                     ldexpf(o[d][4 * r4 + 3] * inv, es)));
         if (hf == 0) lse[(size_t)bh * T + qi] = m * LN2 + logf(l);
     }
 }
@@ -1031,22 +1511,25 @@ int cus_per_xcd() {
 
 // Forward tile configs. wpb: 32-query waves per workgroup (they share every
 // staged K/V tile); snake: snake work order (see work_item); minw: minimum
-// waves per SIMD the register allocation must allow.
+// waves per SIMD the register allocation must allow; h16: the fp16x3 kernel.
 struct FwdCfg {
     const char *name;
     int wpb;
     bool snake;
     int minw;
+    bool h16;
 };
 const FwdCfg FWD_CFGS[] = {
-    {"q128/wg lds-kv mfma32 snake", 4, true, 1},
-    {"q64/wg lds-kv mfma32 snake", 2, true, 1},
-    {"q128/wg lds-kv mfma32", 4, false, 1},
-    {"q128/wg lds-kv mfma32 snake 4w/simd", 4, true, 4},
-    {"q64/wg lds-kv mfma32 snake 4w/simd", 2, true, 4},
+    {"q128/wg lds-kv mfma32 snake", 4, true, 1, false},
+    {"q64/wg lds-kv mfma32 snake", 2, true, 1, false},
+    {"q128/wg lds-kv mfma32", 4, false, 1, false},
+    {"q128/wg lds-kv mfma32 snake 4w/simd", 4, true, 4, false},
+    {"q64/wg lds-kv mfma32 snake 4w/simd", 2, true, 4, false},
+    {"q128/wg lds-kv fp16x3 mfma16 snake", 4, true, 1, true},
+    {"q128/wg lds-kv fp16x3 mfma16 snake 2w/simd", 4, true, 2, true},
 };
 constexpr int N_FWD = sizeof(FWD_CFGS) / sizeof(FWD_CFGS[0]);
-constexpr int FWD_DEFAULT = 0;
+constexpr int FWD_DEFAULT = 5;
 
 // Backward configs. fused: dK/dV and dQ workgroups in one launch; ds_ws:
 // the dK/dV pass stores dS in a library-owned workspace and dQ = scale dS K
@@ -1176,9 +1659,27 @@ void run_fwd(float *out, float *lse, const float *qkv, int B, int T, int NH) {
                 lse, qkv, T, NH, BH, qscale, cus_per_xcd(), order);
 }
 
+template <int HS, int WPB, int MINW>
+void run_fwd_h(float *out, float *lse, const float *qkv, int B, int T, int NH) {
+    const int BH = B * NH;
+    const float qscale = (1.0f / sqrtf((float)HS)) * LOG2E;
+    const size_t smem = FwdSmemH<HS>::bytes(WPB);
+    auto kern = flash_fwd_h_k<HS, WPB, MINW>;
+    bmb::allow_smem(kern, smem);
+    const unsigned *order = fwd_order(T, WPB, BH, wgs_per_cu(kern, WPB * 64, smem));
+    bmb::launch(kern, dim3(grid_blocks(BH, T, 32 * WPB)), dim3(WPB * 64), smem, nullptr, out,
+                lse, qkv, T, NH, BH, qscale, cus_per_xcd(), order);
+}
+
 template <int HS>
 bool fwd_hs(int cfg, float *out, float *lse, const float *qkv, int B, int T, int NH) {
     const FwdCfg &c = FWD_CFGS[cfg];
+    if (c.h16) {
+        if (c.wpb == 4 && c.minw == 1) run_fwd_h<HS, 4, 1>(out, lse, qkv, B, T, NH);
+        else if (c.wpb == 4 && c.minw == 2) run_fwd_h<HS, 4, 2>(out, lse, qkv, B, T, NH);
+        else return false;
+        return true;
+    }
 #define BMB_FWD(W, S, M)                                                       \
     if (c.wpb == W && c.snake == S && c.minw == M) {                           \
         run_fwd<HS, W, S, M>(out, lse, qkv, B, T, NH);                         \

@@ -112,6 +112,52 @@ def test_every_forward_config(gpu, cfg):
     _case(3, 200, 256, 2, 4321, 8765, fcfg=cfg)  # hs 128, ragged T
 
 
+def _range_inputs(kind, B, T, C):
+    """qkv with magnitudes that a plain fp16 conversion would lose: whole
+    inputs far above 65504 or below fp16's normal range, and single key rows
+    (one 32-key tile's worth) of K and V scaled up or down by up to 2^40 or
+    zeroed, which moves the per-tile and running exponents mid-sequence."""
+    qkv = O.fill_xorshift(B * T * 3 * C, 1234).reshape(B, T, 3 * C).astype(np.float64)
+    if kind == "big":
+        qkv *= 1e4
+    elif kind == "small":
+        qkv *= 1e-4
+    elif kind == "tiny":
+        qkv *= 1e-30
+    elif kind == "mixed":
+        k, v = qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
+        k[:, 40:72] *= 2.0 ** 20     # one tile of loud keys
+        v[:, 100:130] *= 2.0 ** 40   # V grows late: the running exponent moves
+        v[:, 10:20] *= 2.0 ** -40    # quiet values inside a tile
+        v[:, 140:180] = 0.0          # a tile of zero values
+        k[:, 200:232] = 0.0          # a tile of zero keys
+        qkv[:, 5:9, :C] *= 2.0 ** -30  # quiet queries
+    return qkv.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["big", "small", "tiny", "mixed"])
+def test_forward_input_range(gpu, kind):
+    """Every forward config against the fp64 oracle on inputs far from unit
+    scale. out is held to the reference's normwise 1e-5. lse is a score-sized
+    quantity: an fp32 dot product is only exact to ~2^-24 sum_d |q_d k_d|,
+    whatever the cancellation, so its error is held to 1e-5 of
+    max(1, max_j sum_d |q_id k_jd| / sqrt(hs)) over the query's keys."""
+    B, T, C, NH = 2, 257, 256, 4
+    hs = C // NH
+    qkv = _range_inputs(kind, B, T, C)
+    ref_o, ref_l = O.attn_fwd_f64(qkv, B, T, C, NH)
+    x = np.abs(qkv.astype(np.float64)).reshape(B, T, 3, NH, hs)
+    qa, ka = x[:, :, 0].transpose(0, 2, 1, 3), x[:, :, 1].transpose(0, 2, 1, 3)
+    mag = (qa @ ka.transpose(0, 1, 3, 2)) / np.sqrt(hs)        # (B, NH, T, T)
+    mag = np.where(np.tril(np.ones((T, T), bool)), mag, 0.0).max(axis=3)
+    for cfg in range(len(bmb.flash_configs())):
+        _, out, lse = _run_fwd(qkv, B, T, C, NH, cfg)
+        eo, bad = O.normwise(out.get().reshape(B, T, C), ref_o)
+        el = np.max(np.abs(lse.get().reshape(B, NH, T) - ref_l) / np.maximum(1.0, mag))
+        print("%s cfg %d: out %.2e lse %.2e" % (kind, cfg, eo, el))
+        assert bad == 0 and eo < TOL and el < 1e-5, (kind, cfg, eo, el)
+
+
 @pytest.mark.parametrize("cfg", range(MAX_CFGS))
 def test_every_backward_config(gpu, cfg):
     if cfg >= len(bmb.flash_bwd_configs()):
