@@ -1491,6 +1491,692 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
     }
 }
 
+// ------------------------------------------------------ backward, fp16x3
+//
+// The default backward on v_mfma_f32_32x32x16_f16 with fp16 hi/lo operands,
+// as the fp16x3 forward above: three passes.
+//  1. flash_dsum_h_k: D = rowsum(dO * O), and per 32-row tile the largest
+//     |Q|, |dO| and |K|, from which the other passes take the tiles'
+//     power-of-two scales (no cross-wave reduction there).
+//  2. dK/dV (kv_tile_h): per key block, streaming query tiles. S = Q K^T and
+//     dP = dO V^T contract over head dims (A: Q / dO rows in LDS, B: the
+//     wave's own K / V rows in registers, per-key scaled); P and dS as in the
+//     fp32 pass; dV += P^T dO and dK += dS^T Q contract over the tile's 32
+//     queries, so Q and dO are also staged transposed (Q^T, dO^T: 8 queries
+//     of one dim per 128-bit read, in the slot order of the forward's V^T).
+//     P^T and dS^T are already A operands (lanes hold keys). dS is stored, in
+//     fp32 with its tile's exponent, for pass 3.
+//  3. dQ (bwd_dq_h_block): dQ = scale dS K from the stored tiles (A: dS rows
+//     from HBM, split on the fly; B: K^T staged in LDS).
+// Scaling: every staged tile and the register operands carry powers of two
+// that put their largest magnitude in [2^13, 2^14); accumulators are kept at
+// the scale of the largest product exponent seen so far (dV: dO's, dK and dQ:
+// dS's times Q's or K's), rescaled when it grows, so no operand exceeds 2^15.
+
+// Per (head, 32-row tile): D rows as flash_dsum_k, and tmax = (max |Q|,
+// max |dO|, max |K|, max |D|). A workgroup is one tile: 32 rows x HS/4 lanes.
+template <int HS>
+__global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
+    float *__restrict__ dsum, float4 *__restrict__ tmax, const float *__restrict__ dout,
+    const float *__restrict__ out, const float *__restrict__ qkv, int T, int NH,
+    float *__restrict__ dqkv, int blk_rows, unsigned long long kv_zero,
+    unsigned long long q_zero) {
+    constexpr int LPR = HS / 4, NT = 32 * LPR, NW = NT / 64;
+    __shared__ float red[4][NW];
+    const int ntiles = (T + 31) / 32;
+    const int tile = blockIdx.x % ntiles, bh = blockIdx.x / ntiles;
+    const int tid = threadIdx.x, sub = tid % LPR;
+    const int t = tile * 32 + tid / LPR;
+    const int h = bh % NH, b = bh / NH;
+    const size_t C = (size_t)NH * HS;
+    float s = 0.0f, mq = 0.0f, mo = 0.0f, mk = 0.0f;
+    if (t < T) {
+        const size_t off = ((size_t)b * T + t) * C + (size_t)h * HS + sub * 4;
+        const float4 a = bmb::ld4(dout + off), c = bmb::ld4(out + off);
+        s = a.x * c.x + a.y * c.y + a.z * c.z + a.w * c.w;
+        mo = absmax4(a);
+        const float *qr = qkv + ((size_t)b * T + t) * 3 * C + (size_t)h * HS + sub * 4;
+        mq = absmax4(bmb::ld4(qr));
+        mk = absmax4(bmb::ld4(qr + C));
+    }
+#pragma unroll
+    for (int w = 1; w < LPR; w <<= 1) s += __shfl_xor(s, w);
+    if (t < T && sub == 0) dsum[(size_t)bh * T + t] = s;
+    mq = wave_max_nonneg(mq);
+    mo = wave_max_nonneg(mo);
+    mk = wave_max_nonneg(mk);
+    float md = wave_max_nonneg(fabsf(s));
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = mq;
+        red[1][tid >> 6] = mo;
+        red[2][tid >> 6] = mk;
+        red[3][tid >> 6] = md;
+    }
+    __syncthreads();
+    if (tid == 0) {
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mq = fmaxf(mq, red[0][w]);
+            mo = fmaxf(mo, red[1][w]);
+            mk = fmaxf(mk, red[2][w]);
+            md = fmaxf(md, red[3][w]);
+        }
+        tmax[(size_t)bh * ntiles + tile] = make_float4(mq, mo, mk, md);
+    }
+    if (t < T && (kv_zero | q_zero) != 0) {
+        const int blk = t / blk_rows;
+        float *r = dqkv + ((size_t)b * T + t) * 3 * C + (size_t)h * HS + sub * 4;
+        if (blk < 64 && ((q_zero >> blk) & 1)) bmb::st4(r, zero4());
+        if (blk < 64 && ((kv_zero >> blk) & 1)) {
+            bmb::st4(r + C, zero4());
+            bmb::st4(r + 2 * C, zero4());
+        }
+    }
+}
+
+template <int HS>
+struct BwdSmemH {
+    static constexpr int LDR = HS + 8;  // halves per row-major row (+16 bytes)
+    static constexpr int LDT = 32 + 8;  // halves per transposed row (+16 bytes)
+    static constexpr int RPLANE = 32 * LDR * 2;  // bytes
+    static constexpr int TPLANE = HS * LDT * 2;
+    // dK/dV pass: Q hi/lo, dO hi/lo (row-major), Q^T hi/lo, dO^T hi/lo,
+    // lse * log2 e, D (32 floats each).
+    static constexpr int OFF_QL = RPLANE, OFF_OH = 2 * RPLANE, OFF_OL = 3 * RPLANE;
+    static constexpr int OFF_QTH = 4 * RPLANE, OFF_QTL = OFF_QTH + TPLANE;
+    static constexpr int OFF_OTH = OFF_QTH + 2 * TPLANE, OFF_OTL = OFF_QTH + 3 * TPLANE;
+    static constexpr int OFF_L = OFF_QTH + 4 * TPLANE, OFF_D = OFF_L + 128;
+    static constexpr int KV_BUF = OFF_D + 128;
+    // dQ pass: K^T hi/lo.
+    static constexpr int Q_BUF = 2 * TPLANE;
+    static constexpr size_t KV_BYTES = 2 * (size_t)KV_BUF, Q_BYTES = 2 * (size_t)Q_BUF;
+};
+
+// Half-index of key kk in a K^T row d of the dQ pass: natural order, 16-byte
+// chunks XOR-swizzled by d/16 as in vt_pos.
+__device__ __forceinline__ int kt_pos(int d, int kk) { return kk ^ (((d >> 4) & 3) << 3); }
+
+// Split a scaled pair and store it in two planes (hi at off, lo at off + dlo).
+__device__ __forceinline__ void put2(char *buf, int off, int dlo, float a, float b) {
+    unsigned hi, lo;
+    split2(a, b, hi, lo);
+    *reinterpret_cast<unsigned *>(buf + off) = hi;
+    *reinterpret_cast<unsigned *>(buf + off + dlo) = lo;
+}
+
+// A 32-row tile of Q and dO (and its lse, D) for the dK/dV pass, in flight to
+// LDS. Thread mapping as KVTileH: float4 column c of rows 2p, 2p+1.
+template <int HS, int NT>
+struct QOTileH {
+    static constexpr int G = HS / 4;
+    static constexpr int PAIRS = NT / G;
+    static constexpr int PASSES = (16 + PAIRS - 1) / PAIRS;
+    float4 q[PASSES][2], o[PASSES][2];
+    float lv;
+
+    __device__ __forceinline__ static bool has(int p) { return PAIRS * PASSES <= 16 || p < 16; }
+
+    __device__ __forceinline__ void load(const float *qb, const float *ob, size_t rs, size_t os,
+                                         int nrows, int tid, const float *lrow,
+                                         const float *drow, int q0, int T) {
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (!has(p)) {
+                    q[ps][j] = o[ps][j] = zero4();
+                    continue;
+                }
+                const int r = min(2 * p + j, nrows - 1);
+                q[ps][j] = ld4_at(qb, 4u * ((unsigned)r * (unsigned)rs + c));
+                o[ps][j] = ld4_at(ob, 4u * ((unsigned)r * (unsigned)os + c));
+            }
+        }
+        if (tid < 64) {
+            const int qq = q0 + (tid & 31);
+            lv = qq < T ? (tid < 32 ? lrow[qq] : drow[qq]) : 0.0f;
+        }
+    }
+
+    // Scale by 2^(14 - eq) and 2^(14 - eo), split, store row-major and
+    // transposed planes; lse (log2 units) and D.
+    __device__ __forceinline__ void store(char *buf, int eq, int eo, int tid) const {
+        using S = BwdSmemH<HS>;
+        const int sq = eq == NOEXP ? 0 : 14 - eq, so = eo == NOEXP ? 0 : 14 - eo;
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+            if (!has(p)) continue;
+            // Row j, dims c..c+3 of Q and dO: hi/lo words (dims c, c+1) and
+            // (c+2, c+3), stored row-major; the transposed words (row 0, row 1)
+            // of each dim are the same halves regrouped.
+            uint2 qh[2], ql[2], oh[2], ol[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float4 a = q[ps][j], bo = o[ps][j];
+                split2(ldexpf(a.x, sq), ldexpf(a.y, sq), qh[j].x, ql[j].x);
+                split2(ldexpf(a.z, sq), ldexpf(a.w, sq), qh[j].y, ql[j].y);
+                split2(ldexpf(bo.x, so), ldexpf(bo.y, so), oh[j].x, ol[j].x);
+                split2(ldexpf(bo.z, so), ldexpf(bo.w, so), oh[j].y, ol[j].y);
+                const int ro = (2 * p + j) * S::LDR * 2 + c * 2;
+                *reinterpret_cast<uint2 *>(buf + ro) = qh[j];
+                *reinterpret_cast<uint2 *>(buf + S::OFF_QL + ro) = ql[j];
+                *reinterpret_cast<uint2 *>(buf + S::OFF_OH + ro) = oh[j];
+                *reinterpret_cast<uint2 *>(buf + S::OFF_OL + ro) = ol[j];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int to = ((c + i) * S::LDT + vt_pos(c + i, 2 * p)) * 2;
+                const unsigned sel = (i & 1) ? 0x07060302u : 0x05040100u;  // high / low halves
+                const unsigned w0 = (i < 2) ? 0 : 1;
+                auto pick = [&](const uint2 (&x)[2]) {
+                    return __builtin_amdgcn_perm(w0 ? x[1].y : x[1].x, w0 ? x[0].y : x[0].x, sel);
+                };
+                *reinterpret_cast<unsigned *>(buf + S::OFF_QTH + to) = pick(qh);
+                *reinterpret_cast<unsigned *>(buf + S::OFF_QTL + to) = pick(ql);
+                *reinterpret_cast<unsigned *>(buf + S::OFF_OTH + to) = pick(oh);
+                *reinterpret_cast<unsigned *>(buf + S::OFF_OTL + to) = pick(ol);
+            }
+        }
+        if (tid < 64) reinterpret_cast<float *>(buf + S::OFF_L)[tid] = tid < 32 ? lv * LOG2E : lv;
+    }
+};
+
+// One 32-query tile of the dK/dV pass for this wave's 32 keys (lane = key
+// l32; register r of S, dP, P, dS holds query qb + res_row(r, hf)).
+// cS, cD: per-lane factors that turn the MFMA sums into log2-unit scores and
+// dP. eq, eo: the tile's exponents of Q and dO; eds: an exponent bounding
+// |dS| over the tile (|dS| <= |dP| + |D| <= HS max|dO| max|V| + max|D|).
+// Ev, Ek: current scales of dv and dk (see the section comment).
+template <int HS, bool MASK>
+__device__ __forceinline__ void kv_tile_h(const char *buf, const h8 (&kh)[HS / 16],
+                                          const h8 (&kl)[HS / 16], const h8 (&vh)[HS / 16],
+                                          const h8 (&vl)[HS / 16], float cS, float cD, int eq,
+                                          int eo, int eds, f32x16 (&dv)[HS / 32],
+                                          f32x16 (&dk)[HS / 32], int &Ev, int &Ek, int qb,
+                                          int key, int T, int l32, int hf,
+                                          float *__restrict__ ds_out) {
+    constexpr int NS = HS / 16, DT = HS / 32;
+    using S = BwdSmemH<HS>;
+    f32x16 s = zero16(), dp = zero16();
+    const char *qr = buf + l32 * S::LDR * 2 + hf * HS;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        const h8 qh = *reinterpret_cast<const h8 *>(qr + 16 * st);
+        const h8 ql = *reinterpret_cast<const h8 *>(qr + S::OFF_QL + 16 * st);
+        const h8 oh = *reinterpret_cast<const h8 *>(qr + S::OFF_OH + 16 * st);
+        const h8 ol = *reinterpret_cast<const h8 *>(qr + S::OFF_OL + 16 * st);
+        s = mfma_h(qh, kh[st], s);
+        dp = mfma_h(oh, vh[st], dp);
+        s = mfma_h(qh, kl[st], s);
+        dp = mfma_h(oh, vl[st], dp);
+        s = mfma_h(ql, kh[st], s);
+        dp = mfma_h(ol, vh[st], dp);
+    }
+    // Scales: dv holds sum P dO 2^(29 - Ev), dk holds sum dS Q 2^(14 - Ek).
+    // (Uniform; decided while the score MFMAs run.)
+    const int nv = max(Ev, eo), nk = max(Ek, eq + eds - 15);
+    if (nv > Ev || nk > Ek) {
+        const float av = ldexpf(1.0f, Ev - nv), ak = ldexpf(1.0f, Ek - nk);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                dv[d][r] *= av;
+                dk[d][r] *= ak;
+            }
+        Ev = nv;
+        Ek = nk;
+    }
+    const int gp = eo - Ev + 15, gd = eq - Ek;  // P'' = P 2^gp <= 2^15, dS'' = dS 2^gd <= 2^15
+    float p[16], ds[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 L4 = *reinterpret_cast<const float4 *>(buf + S::OFF_L + 4 * (8 * j + 4 * hf));
+        const float4 D4 = *reinterpret_cast<const float4 *>(buf + S::OFF_D + 4 * (8 * j + 4 * hf));
+        const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
+        const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * j + i;
+            float x = fmaf(s[r], cS, -Lr[i]);
+            if (MASK) {
+                const int q = qb + res_row(r, hf);
+                x = ((key > q) | (q >= T)) ? -INFINITY : x;  // exp2(-inf) = 0
+            }
+            p[r] = exp2_hw(x);
+            ds[r] = p[r] * fmaf(dp[r], cD, -Dr[i]);
+        }
+    }
+    // dS tile for the dQ pass, row-major [query][key]: each half-wave stores
+    // 32 consecutive keys of one query row per instruction.
+    float *dsl = ds_out + 128 * hf + l32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dsl[(8 * (r >> 2) + (r & 3)) * 32] = ds[r];
+    h8 ph[2], pl[2], dh[2], dl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        unsigned a[4], b[4], c[4], e[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = 8 * ks + 2 * u;
+            split2(ldexpf(p[r], gp), ldexpf(p[r + 1], gp), a[u], b[u]);
+            split2(ldexpf(ds[r], gd), ldexpf(ds[r + 1], gd), c[u], e[u]);
+        }
+        ph[ks] = __builtin_bit_cast(h8, make_uint4(a[0], a[1], a[2], a[3]));
+        pl[ks] = __builtin_bit_cast(h8, make_uint4(b[0], b[1], b[2], b[3]));
+        dh[ks] = __builtin_bit_cast(h8, make_uint4(c[0], c[1], c[2], c[3]));
+        dl[ks] = __builtin_bit_cast(h8, make_uint4(e[0], e[1], e[2], e[3]));
+    }
+    // dV += P^T dO, dK += dS^T Q: B operands dO^T / Q^T rows (dim d*32 + l32).
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+        const int row = d * 32 + l32;
+        const int sw = ((row >> 4) & 3) << 4;
+        const char *orow = buf + S::OFF_OTH + row * S::LDT * 2;
+        const char *qrow = buf + S::OFF_QTH + row * S::LDT * 2;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int off = (32 * ks + 16 * hf) ^ sw;
+            const h8 oh = *reinterpret_cast<const h8 *>(orow + off);
+            const h8 ol = *reinterpret_cast<const h8 *>(orow + S::TPLANE + off);
+            const h8 qh = *reinterpret_cast<const h8 *>(qrow + off);
+            const h8 ql = *reinterpret_cast<const h8 *>(qrow + S::TPLANE + off);
+            dv[d] = mfma_h(ph[ks], oh, dv[d]);
+            dk[d] = mfma_h(dh[ks], qh, dk[d]);
+            dv[d] = mfma_h(ph[ks], ol, dv[d]);
+            dk[d] = mfma_h(dh[ks], ql, dk[d]);
+            dv[d] = mfma_h(pl[ks], oh, dv[d]);
+            dk[d] = mfma_h(dl[ks], qh, dk[d]);
+        }
+    }
+}
+
+// Loads of per-tile values at a uniform address through the vector memory
+// path: a scalar load would share its wait counter with LDS accesses, so the
+// first LDS wait after it would also wait for its global-memory latency.
+template <typename V>
+__device__ __forceinline__ V vload(const V *p, size_t i) {
+    unsigned lo = (unsigned)i;
+    asm volatile("" : "+v"(lo));  // a VGPR index: the compiler emits a vector load
+    return p[((i >> 32) << 32) | lo];
+}
+
+// Exponent of the largest magnitude of a tile from the dsum pass's maxima
+// (component c: 0 Q, 1 dO, 2 K, 3 D).
+__device__ __forceinline__ int tile_exp(const float4 *tmax, int bh, int ntiles, int tile, int c) {
+    const float4 v = vload(tmax, (size_t)bh * ntiles + tile);
+    return max_exp(c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w);
+}
+
+// dK, dV for the WPB*32 keys of key block kblk of head bh (fp16x3), storing
+// the dS tiles in ws and the exponent bounding each in ws_exp.
+template <int HS, int WPB>
+__device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ dqkv,
+                                               const float *__restrict__ qkv,
+                                               const float *__restrict__ dout,
+                                               const float *__restrict__ lse,
+                                               const float *__restrict__ dsum,
+                                               const float4 *__restrict__ tmax, int T, int NH,
+                                               int kblk, int bh, float scale, float qscale,
+                                               float *__restrict__ ws, int *__restrict__ ws_exp,
+                                               int tq0, int tq1, bool accumulate) {
+    constexpr int NT = WPB * 64, KB = 32 * WPB, HH = HS / 2, NS = HS / 16, DT = HS / 32;
+    using S = BwdSmemH<HS>;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int b = bh / NH, h = bh % NH, C = NH * HS;
+    const size_t rs = 3 * (size_t)C;
+    const float *base = qkv + (size_t)b * T * rs + h * HS;
+    const float *dob = dout + (size_t)b * T * C + h * HS;
+    const float *lrow = lse + (size_t)bh * T;
+    const float *drow = dsum + (size_t)bh * T;
+    const int ntiles = (T + 31) / 32;
+
+    const int k0w = kblk * KB + wave * 32, key = k0w + l32;
+    const bool active = k0w < T;
+    // B operands: this lane's key row of K (times qscale) and V, each scaled
+    // by the key's power of two and split. evw: exponent of the wave's max |V|.
+    h8 kh[NS], kl[NS], vh[NS], vl[NS];
+    float fk, fv;
+    int evw;
+    {
+        float kq[HH], vq[HH];
+        float ak = 0.0f, av = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HH; j += 4) {
+            float4 kv = zero4(), vv = zero4();
+            if (key < T) {
+                kv = bmb::ld4(base + (size_t)key * rs + C + hf * HH + j);
+                vv = bmb::ld4(base + (size_t)key * rs + 2 * C + hf * HH + j);
+            }
+            kq[j + 0] = kv.x * qscale; kq[j + 1] = kv.y * qscale;
+            kq[j + 2] = kv.z * qscale; kq[j + 3] = kv.w * qscale;
+            vq[j + 0] = vv.x; vq[j + 1] = vv.y; vq[j + 2] = vv.z; vq[j + 3] = vv.w;
+            ak = fmaxf(ak, absmax4(make_float4(kq[j], kq[j + 1], kq[j + 2], kq[j + 3])));
+            av = fmaxf(av, absmax4(vv));
+        }
+        evw = max_exp(wave_max_nonneg(av));
+        const int ek = max_exp(pair_max(ak)), ev = max_exp(pair_max(av));
+        fk = ek == NOEXP ? 0.0f : ldexpf(1.0f, ek - 14);
+        fv = ev == NOEXP ? 0.0f : ldexpf(1.0f, ev - 14);
+        const int sk = ek == NOEXP ? 0 : 14 - ek, sv = ev == NOEXP ? 0 : 14 - ev;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            unsigned a[4], bb[4], c[4], e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = 8 * st + 2 * u;
+                split2(ldexpf(kq[j], sk), ldexpf(kq[j + 1], sk), a[u], bb[u]);
+                split2(ldexpf(vq[j], sv), ldexpf(vq[j + 1], sv), c[u], e[u]);
+            }
+            kh[st] = __builtin_bit_cast(h8, make_uint4(a[0], a[1], a[2], a[3]));
+            kl[st] = __builtin_bit_cast(h8, make_uint4(bb[0], bb[1], bb[2], bb[3]));
+            vh[st] = __builtin_bit_cast(h8, make_uint4(c[0], c[1], c[2], c[3]));
+            vl[st] = __builtin_bit_cast(h8, make_uint4(e[0], e[1], e[2], e[3]));
+        }
+    }
+
+    f32x16 dv[DT], dk[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) { dv[d] = zero16(); dk[d] = zero16(); }
+    int Ev = -2000, Ek = -2000;  // below every product exponent
+
+    const int nqt = tq1 - tq0;
+    QOTileH<HS, NT> qo;
+    // Tile t (clamped to the last) of Q and dO, and its exponents.
+    auto load_tile = [&](int t) {
+        const int q0 = (tq0 + min(t, nqt - 1)) * 32;
+        qo.load(base + (size_t)q0 * rs, dob + (size_t)q0 * C, rs, C, min(32, T - q0), tid, lrow,
+                drow, q0, T);
+    };
+    // (kept in scalar registers: the values are uniform)
+    auto uni = [](float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); };
+    auto tile_max = [&](int t) {
+        const float4 v = vload(tmax, (size_t)bh * ntiles + tq0 + min(t, nqt - 1));
+        return make_float4(uni(v.x), uni(v.y), uni(v.z), uni(v.w));
+    };
+    // The tile maxima are read one tile ahead (their loads would otherwise sit
+    // right before their first use).
+    float4 m_cur = tile_max(0);
+    load_tile(0);
+    qo.store(smem, max_exp(m_cur.x), max_exp(m_cur.y), tid);
+    float4 m_next = tile_max(1);
+    __syncthreads();
+
+    for (int t = 0; t < nqt; ++t) {
+        const int qb = (tq0 + t) * 32;
+        load_tile(t + 1);
+        const float4 m_after = tile_max(t + 2);
+        if (active && qb >= k0w) {
+            const char *buf = smem + (t & 1) * S::KV_BUF;
+            const int eq = max_exp(m_cur.x), eo = max_exp(m_cur.y);
+            const float cS = ldexpf(fk, eq == NOEXP ? -2000 : eq - 14);
+            const float cD = ldexpf(fv, eo == NOEXP ? -2000 : eo - 14);
+            // |dS| < HS 2^(eo + evw) + max|D|
+            const int eds = (eo == NOEXP || evw == NOEXP)
+                                ? max_exp(m_cur.w)
+                                : max_exp(ldexpf((float)HS, eo + evw) + m_cur.w);
+            const size_t dti = (size_t)bh * ds_tiles_per_head(T) +
+                               (size_t)(qb >> 5) * ((qb >> 5) + 1) / 2 + (k0w >> 5);
+            float *dso = ws + dti * 1024;
+            if (l32 == 0 && hf == 0) ws_exp[dti] = eds;
+            if (qb == k0w || qb + 32 > T || k0w + 32 > T)  // diagonal or ragged
+                kv_tile_h<HS, true>(buf, kh, kl, vh, vl, cS, cD, eq, eo, eds, dv, dk, Ev, Ek, qb,
+                                    key, T, l32, hf, dso);
+            else
+                kv_tile_h<HS, false>(buf, kh, kl, vh, vl, cS, cD, eq, eo, eds, dv, dk, Ev, Ek,
+                                     qb, key, T, l32, hf, dso);
+        }
+        // Stage tile t+1 (past the last tile: the last again, into the buffer
+        // nobody reads).
+        qo.store(smem + ((t + 1) & 1) * S::KV_BUF, max_exp(m_next.x), max_exp(m_next.y), tid);
+        m_cur = m_next;
+        m_next = m_after;
+        __syncthreads();
+    }
+
+    if (!active) return;
+    const int sv = Ev - 29, sk = Ek - 14;
+    float *dkb = dqkv + ((size_t)b * T + k0w) * rs + C + h * HS + l32;
+    auto out = [&](auto &&put) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float *dkp = dkb + (size_t)res_row(r, hf) * rs;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                put(dkp + d * 32, ldexpf(dk[d][r], sk) * scale);
+                put(dkp + C + d * 32, ldexpf(dv[d][r], sv));
+            }
+        }
+    };
+    if (k0w + 32 <= T) {
+        if (accumulate) out([](float *a, float v) { atomicAdd(a, v); });
+        else out([](float *a, float v) { *a = v; });
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (k0w + res_row(r, hf) >= T) continue;
+            float *dkp = dkb + (size_t)res_row(r, hf) * rs;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const float vk = ldexpf(dk[d][r], sk) * scale, vv = ldexpf(dv[d][r], sv);
+                if (accumulate) {
+                    atomicAdd(dkp + d * 32, vk);
+                    atomicAdd(dkp + C + d * 32, vv);
+                } else {
+                    dkp[d * 32] = vk;
+                    dkp[C + d * 32] = vv;
+                }
+            }
+        }
+    }
+}
+
+// dQ for the WPB*32 queries of query block qblk of head bh from the stored dS
+// tiles (fp16x3): dQ = scale dS K. A operand: dS row l32 of the wave's tile,
+// keys 16 ks + 8 hf + 0..7 (step ks), read from HBM PF tiles ahead; B operand:
+// K^T rows from LDS (the same keys). dq holds sum dS K 2^(14 - F), F the
+// largest exponent of dS times K seen so far minus 15.
+template <int HS, int WPB>
+__device__ __forceinline__ void bwd_dq_h_block(char *smem, float *__restrict__ dqkv,
+                                               const float *__restrict__ qkv,
+                                               const float *__restrict__ ws,
+                                               const int *__restrict__ ws_exp,
+                                               const float4 *__restrict__ tmax, int T, int NH,
+                                               int qblk, int bh, float scale, int tk0, int tk1,
+                                               bool accumulate) {
+    constexpr int NT = WPB * 64, DT = HS / 32;
+    constexpr int G = HS / 4, PAIRS = NT / G, PASSES = (16 + PAIRS - 1) / PAIRS;
+    using S = BwdSmemH<HS>;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int b = bh / NH, h = bh % NH, C = NH * HS;
+    const size_t rs = 3 * (size_t)C;
+    const float *base = qkv + (size_t)b * T * rs + h * HS;
+    const int ntiles = (T + 31) / 32;
+
+    const int qtw = qblk * WPB + wave, q0w = qtw * 32;
+    const bool active = q0w < T;
+    const int nkt = tk1 - tk0;
+    const int my_nkt = active ? max(0, min(tk1, qtw + 1) - tk0) : 0;
+
+    f32x16 dq[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) dq[d] = zero16();
+    int F = -2000;
+
+    // dS ring, PF tiles ahead (see bwd_dq_from_ds_block); every load issued.
+    constexpr int PF = 3;
+    const int last = max(my_nkt - 1, 0);
+    const size_t tile0 = (size_t)bh * ds_tiles_per_head(T) +
+                         (my_nkt > 0 ? (size_t)qtw * (qtw + 1) / 2 + tk0 : 0);
+    const float *wsw = ws + tile0 * 1024;
+    const int *wse = ws_exp + tile0;
+    // keys 8hf..8hf+7 and 16+8hf..16+8hf+7 of query row l32
+    const unsigned lane_off = 4u * (l32 * 32 + 8 * hf);
+    float4 ring[PF][4];
+    auto ds_load = [&](float4 (&r)[4], int j) {
+        const unsigned tb = 4096u * min(j, last) + lane_off;
+        r[0] = ld4_at(wsw, tb);
+        r[1] = ld4_at(wsw, tb + 16u);
+        r[2] = ld4_at(wsw, tb + 64u);
+        r[3] = ld4_at(wsw, tb + 80u);
+    };
+    // K tile loads one tile ahead: thread holds float4 column c of keys 2p, 2p+1.
+    float4 kr[PASSES][2];
+    auto k_load = [&](int j) {
+        const int k0 = (tk0 + min(j, nkt - 1)) * 32, nr = min(32, T - k0);
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                if (PAIRS * PASSES > 16 && p >= 16) { kr[ps][jj] = zero4(); continue; }
+                const int r = min(2 * p + jj, nr - 1);
+                kr[ps][jj] = ld4_at(base + (size_t)k0 * rs + C, 4u * ((unsigned)r * (unsigned)rs + c));
+            }
+        }
+    };
+    auto k_store = [&](char *buf, int e) {
+        const int sk = e == NOEXP ? 0 : 14 - e;
+        const int c = (tid % G) * 4;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int p = tid / G + ps * PAIRS;
+            if (PAIRS * PASSES > 16 && p >= 16) continue;
+            const float a0[4] = {kr[ps][0].x, kr[ps][0].y, kr[ps][0].z, kr[ps][0].w};
+            const float a1[4] = {kr[ps][1].x, kr[ps][1].y, kr[ps][1].z, kr[ps][1].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                put2(buf, ((c + i) * S::LDT + kt_pos(c + i, 2 * p)) * 2, S::TPLANE,
+                     ldexpf(a0[i], sk), ldexpf(a1[i], sk));
+        }
+    };
+    // Exponents of K tile j and of the wave's dS tile j, read ahead of use.
+    auto kexp = [&](int j) { return tile_exp(tmax, bh, ntiles, tk0 + min(j, nkt - 1), 2); };
+    int eds_ring[PF];
+    k_load(0);
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        ds_load(ring[j], j);
+        eds_ring[j] = vload(wse, (size_t)min(j, last));
+    }
+    int ek_cur = kexp(0), ek_next = kexp(1);
+    k_store(smem, ek_cur);
+    k_load(1);
+    __syncthreads();
+
+    for (int t0 = 0; t0 < nkt; t0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int t = t0 + u;
+            if (t >= nkt) break;
+            const int ek_after = kexp(t + 2);
+            if (t < my_nkt) {
+                const char *buf = smem + (t & 1) * S::Q_BUF;
+                const int eds = __builtin_amdgcn_readfirstlane(eds_ring[u]);
+                const int ek = ek_cur;
+                const int G2 = (eds == NOEXP || ek == NOEXP) ? -2000 : eds + ek - 15;
+                if (G2 > F) {
+                    const float a = ldexpf(1.0f, F - G2);
+#pragma unroll
+                    for (int d = 0; d < DT; ++d)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) dq[d][r] *= a;
+                    F = G2;
+                }
+                const int sh = ek == NOEXP ? -2000 : ek - F;  // dS'' = dS 2^sh <= 2^15
+                const float v[16] = {ring[u][0].x, ring[u][0].y, ring[u][0].z, ring[u][0].w,
+                                     ring[u][1].x, ring[u][1].y, ring[u][1].z, ring[u][1].w,
+                                     ring[u][2].x, ring[u][2].y, ring[u][2].z, ring[u][2].w,
+                                     ring[u][3].x, ring[u][3].y, ring[u][3].z, ring[u][3].w};
+                h8 ah[2], al[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    unsigned x[4], y[4];
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        split2(ldexpf(v[8 * ks + 2 * w], sh), ldexpf(v[8 * ks + 2 * w + 1], sh),
+                               x[w], y[w]);
+                    ah[ks] = __builtin_bit_cast(h8, make_uint4(x[0], x[1], x[2], x[3]));
+                    al[ks] = __builtin_bit_cast(h8, make_uint4(y[0], y[1], y[2], y[3]));
+                }
+#pragma unroll
+                for (int d = 0; d < DT; ++d) {
+                    const int row = d * 32 + l32;
+                    const int sw = ((row >> 4) & 3) << 4;
+                    const char *kt = buf + row * S::LDT * 2;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const int off = (32 * ks + 16 * hf) ^ sw;
+                        const h8 bh8 = *reinterpret_cast<const h8 *>(kt + off);
+                        const h8 bl8 = *reinterpret_cast<const h8 *>(kt + S::TPLANE + off);
+                        dq[d] = mfma_h(ah[ks], bh8, dq[d]);
+                        dq[d] = mfma_h(ah[ks], bl8, dq[d]);
+                        dq[d] = mfma_h(al[ks], bh8, dq[d]);
+                    }
+                }
+            }
+            ds_load(ring[u], t + PF);
+            eds_ring[u] = vload(wse, (size_t)min(t + PF, last));
+            k_store(smem + ((t + 1) & 1) * S::Q_BUF, ek_next);
+            k_load(t + 2);
+            ek_cur = ek_next;
+            ek_next = ek_after;
+            __syncthreads();
+        }
+    }
+
+    if (!active) return;
+    const int sq = F - 14;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int q = q0w + res_row(r, hf);
+        if (q >= T) continue;
+        float *dst = dqkv + ((size_t)b * T + q) * rs + h * HS;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            const float val = ldexpf(dq[d][r], sq) * scale;
+            if (accumulate) atomicAdd(dst + d * 32 + l32, val);
+            else dst[d * 32 + l32] = val;
+        }
+    }
+}
+
+// MODE 0: dK/dV (storing dS), MODE 1: dQ from dS; persistent workgroups as
+// flash_bwd_k's MODE 3 / 4.
+template <int HS, int WPB, int MODE, int MINW>
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
+flash_bwd_h_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
+              const float *__restrict__ dout, const float *__restrict__ lse,
+              const float *__restrict__ dsum, const float4 *__restrict__ tmax, int T, int NH,
+              float scale, float qscale, float *__restrict__ ws, int *__restrict__ ws_exp,
+              const Items items, const int *__restrict__ sched_off,
+              const unsigned *__restrict__ sched_ent) {
+    extern __shared__ float smem[];
+    char *sm = reinterpret_cast<char *>(smem);
+    const int bid = blockIdx.x;
+    const int e0 = sched_off[bid], e1 = sched_off[bid + 1];
+    for (int e = e0; e < e1; ++e) {
+        const unsigned ent = sched_ent[e];
+        const int it = (int)(ent & 0xffffu);
+        const int bh = (int)(ent >> 16);
+        if (e > e0) __syncthreads();  // the previous item's last LDS reads
+        if (MODE == 0)
+            bwd_kv_h_block<HS, WPB>(sm, dqkv, qkv, dout, lse, dsum, tmax, T, NH, items.blk[it],
+                                    bh, scale, qscale, ws, ws_exp, items.t0[it], items.t1[it],
+                                    items.split[it]);
+        else
+            bwd_dq_h_block<HS, WPB>(sm, dqkv, qkv, ws, ws_exp, tmax, T, NH, items.blk[it], bh,
+                                    scale, items.t0[it], items.t1[it], items.split[it]);
+    }
+}
+
 // ------------------------------------------------------------- host side
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1540,19 +2226,21 @@ struct BwdCfg {
     bool fused;
     int minw;
     bool ds_ws;
+    bool h16;  // the fp16x3 kernels (dS stored)
 };
 const BwdCfg BWD_CFGS[] = {
-    {"kv128+q128/wg fused lds mfma32 2w/simd", 4, true, 2, false},
-    {"kv64+q64/wg fused lds mfma32 2w/simd", 2, true, 2, false},
-    {"kv128/wg then q128/wg lds mfma32 2w/simd", 4, false, 2, false},
-    {"kv64/wg then q64/wg lds mfma32 2w/simd", 2, false, 2, false},
-    {"kv128+q128/wg fused lds mfma32", 4, true, 1, false},
-    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32 2w/simd", 4, false, 2, true},
-    {"kv64/wg storing dS, then dQ=dS.K q64/wg, mfma32 2w/simd", 2, false, 2, true},
-    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32", 4, false, 1, true},
+    {"kv128+q128/wg fused lds mfma32 2w/simd", 4, true, 2, false, false},
+    {"kv64+q64/wg fused lds mfma32 2w/simd", 2, true, 2, false, false},
+    {"kv128/wg then q128/wg lds mfma32 2w/simd", 4, false, 2, false, false},
+    {"kv64/wg then q64/wg lds mfma32 2w/simd", 2, false, 2, false, false},
+    {"kv128+q128/wg fused lds mfma32", 4, true, 1, false, false},
+    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32 2w/simd", 4, false, 2, true, false},
+    {"kv64/wg storing dS, then dQ=dS.K q64/wg, mfma32 2w/simd", 2, false, 2, true, false},
+    {"kv128/wg storing dS, then dQ=dS.K q128/wg, mfma32", 4, false, 1, true, false},
+    {"kv128/wg storing dS, then dQ=dS.K q128/wg, fp16x3 mfma16 2w/simd", 4, false, 2, true, true},
 };
 constexpr int N_BWD = sizeof(BWD_CFGS) / sizeof(BWD_CFGS[0]);
-constexpr int BWD_DEFAULT = 5;
+constexpr int BWD_DEFAULT = 8;  // the fp16x3 backward
 
 // dS workspace: leased from the library's per-device pool for one backward
 // call (workspace.hpp). Both passes that use it are queued on the null stream
@@ -1964,10 +2652,54 @@ bool run_bwd(const BwdCfg &c, float *dqkv, float *dsum, const float *dout, const
     return true;
 }
 
+// The fp16x3 backward: dsum + tile maxima, dK/dV storing dS, dQ from dS.
+// Workspace (one lease): the dS tiles (fp32), their exponents, the tile
+// maxima.
+template <int HS, int WPB, int MINW>
+bool run_bwd_h(float *dqkv, float *dsum, const float *dout, const float *qkv, const float *out,
+               const float *lse, int B, int T, int NH) {
+    using S = BwdSmemH<HS>;
+    const int BH = B * NH, threads = WPB * 64, ntiles = (T + 31) / 32;
+    auto kkv = flash_bwd_h_k<HS, WPB, 0, MINW>;
+    auto kq = flash_bwd_h_k<HS, WPB, 1, MINW>;
+    bmb::allow_smem(kkv, S::KV_BYTES);
+    bmb::allow_smem(kq, S::Q_BYTES);
+    Sched kv_sc, q_sc;
+    if (!get_sched(true, T, WPB, BH, wgs_per_cu(kkv, threads, S::KV_BYTES), kv_sc) ||
+        !get_sched(false, T, WPB, BH, wgs_per_cu(kq, threads, S::Q_BYTES), q_sc))
+        return false;
+    const size_t nds = (size_t)BH * ds_tiles_per_head(T);
+    const size_t off_exp = nds * 4096, off_max = off_exp + ((nds * 4 + 15) & ~(size_t)15);
+    std::optional<bmb::ScratchLease> lease;
+    lease.emplace(bmb::SCRATCH_FLASH_DS, off_max + (size_t)BH * ntiles * sizeof(float4));
+    char *w = static_cast<char *>(lease->get());
+    if (w == nullptr) return false;  // no workspace: the caller tries another config
+    float *ws = reinterpret_cast<float *>(w);
+    int *ws_exp = reinterpret_cast<int *>(w + off_exp);
+    float4 *tmax = reinterpret_cast<float4 *>(w + off_max);
+    bmb::launch(flash_dsum_h_k<HS>, dim3((unsigned)(BH * ntiles)), dim3(8 * HS), 0, nullptr,
+                dsum, tmax, dout, out, qkv, T, NH, dqkv, 32 * WPB, kv_sc.zero_mask,
+                q_sc.zero_mask);
+    const float scale = 1.0f / sqrtf((float)HS);
+    bmb::launch(kkv, dim3(kv_sc.wgs), dim3(threads), S::KV_BYTES, nullptr, dqkv, qkv, dout, lse,
+                dsum, (const float4 *)tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
+                kv_sc.items, (const int *)kv_sc.off, (const unsigned *)kv_sc.ent);
+    bmb::launch(kq, dim3(q_sc.wgs), dim3(threads), S::Q_BYTES, nullptr, dqkv, qkv, dout, lse,
+                dsum, (const float4 *)tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
+                q_sc.items, (const int *)q_sc.off, (const unsigned *)q_sc.ent);
+    return true;
+}
+
 template <int HS>
 bool bwd_hs(int cfg, float *dqkv, float *dsum, const float *dout, const float *qkv,
             const float *out, const float *lse, int B, int T, int NH) {
     const BwdCfg &c = BWD_CFGS[cfg];
+    if (c.h16) {
+        // (head size 128 needs the whole register file: one wave per SIMD)
+        if (c.wpb == 4 && c.minw == 2)
+            return run_bwd_h<HS, 4, HS == 128 ? 1 : 2>(dqkv, dsum, dout, qkv, out, lse, B, T, NH);
+        return false;
+    }
 #define BMB_BWD(W, M)                                                              \
     if (c.wpb == W && c.minw == M)                                                 \
         return run_bwd<HS, W, M>(c, dqkv, dsum, dout, qkv, out, lse, B, T, NH);

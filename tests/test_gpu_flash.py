@@ -53,12 +53,14 @@ def _run_bwd(d_qkv, out, lse, dout, B, T, C, NH, cfg=None):
 def _check_grads(got, want, C):
     """Normwise error of dq, dk, dv separately (test_flash.cu:292-314).
 
-    The denominator of each slice is floored at 1e-2 of the largest |ref|
-    over all three: where a slice is exactly zero in exact arithmetic
-    (T = 1: a one-key softmax has zero gradient, so dq = dk = 0 and only dv
-    is non-zero) its fp32 rounding noise is measured against the scale of
-    the gradient as a whole instead of against zero."""
-    floor = 1e-2 * float(np.abs(want).max())
+    A slice whose largest |ref| is below 1e-2 of the largest over all three
+    is zero in exact arithmetic (T = 1: a one-key softmax has zero gradient,
+    so dq = dk = 0 and only dv is non-zero); what the kernel returns there is
+    rounding noise of the cancellation dP - D, so it is measured against the
+    scale of the gradient as a whole (the largest |ref|), not against zero.
+    That noise is ~2^-24 of the gradient scale for fp32 products and ~2^-22
+    for the fp16x3 kernels, whose operands carry 22 significant bits."""
+    gmax = float(np.abs(want).max())
     errs = []
     for s, name in enumerate("qkv"):
         g = got[:, :, s * C:(s + 1) * C]
@@ -66,8 +68,8 @@ def _check_grads(got, want, C):
         e, bad = O.normwise(g, w)
         assert bad == 0, "non-finite d%s" % name
         wmax = float(np.abs(w).max()) if w.size else 0.0
-        if wmax < floor:
-            e = float(np.abs(g.astype(np.float64) - w).max()) / floor
+        if wmax < 1e-2 * gmax:
+            e = float(np.abs(g.astype(np.float64) - w).max()) / gmax
         errs.append(e)
     return errs
 
@@ -101,7 +103,7 @@ def test_ragged_shapes(gpu, shape):
     _case(*shape, 4321, 8765)
 
 
-MAX_CFGS = 8  # more than either table holds; ids past the end are skipped
+MAX_CFGS = 10  # more than either table holds; ids past the end are skipped
 
 
 @pytest.mark.parametrize("cfg", range(MAX_CFGS))
