@@ -575,10 +575,6 @@ __device__ __forceinline__ int max_exp(float m) {
     return m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : NOEXP;
 }
 
-__device__ __forceinline__ int pair_max_i(int v) {
-    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
-    return max((int)r[0], (int)r[1]);
-}
 
 constexpr float SOFTMAX_SLACK = 8.0f;  // log2 units a stale running max may lag
 

@@ -7,14 +7,15 @@ namespace bmb {
 
 // C[M,N] = A[M,K] @ W[N,K]^T + bias[N] (row broadcast), the linear layer of
 // src/gpt.cu (gemm(false, true, ...) then bias_forward); when gelu_out is not
-// null it also stores gelu(C) there (the FC layer's gelu_forward). Same fp32
-// results as the three separate passes; null stream, like the reference.
+// null it also stores gelu(C) there (the FC layer's gelu_forward). The product
+// is gemm()'s (bf16x3); bias and GELU are applied in fp32 as the separate
+// passes do; null stream, like the reference.
 void gemm_bias_nt(int M, int N, int K, const float *A, const float *W, const float *bias,
                   float *C, float *gelu_out);
 
 // C[M,N] = gelu_grad(pre, A[M,K] @ B[K,N]) elementwise: the dX GEMM of the
 // FC projection (gemm(false, false, ...)) followed by gelu_backward
-// (src/gpt.cu:331-337), without storing the product. Same fp32 results.
+// (src/gpt.cu:331-337), without storing the product.
 void gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B, const float *pre,
                        float *C);
 
@@ -24,5 +25,23 @@ void gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B, cons
 // shape and the split count).
 void splitk_reduce(float *C, const float *P, int splits, long long mn, int N, float alpha,
                    float beta, hipStream_t stream);
+
+// The same reduce ending in epilogue `epi` (an Epi of mfma_gemm.hpp: bias[N],
+// act = gelu(C) output, pre = the GELU input, as the GEMM epilogues).
+void splitk_reduce_epi(int epi, float *C, const float *P, int splits, long long mn, int N,
+                       float alpha, float beta, hipStream_t stream, const float *bias,
+                       float *act, const float *pre);
+
+// Row-major C[M,N] = epilogue(op(A) @ op(B)) on bf16x3 matrix-core products
+// (sgemm_bf16x3.hip): each fp32 operand split into bf16 hi + lo, three bf16
+// products per term, fp32 accumulation. epi: EPI_BLAS (C = alpha acc +
+// beta C, any transposes), EPI_BIAS / EPI_BIAS_GELU (transB only), or
+// EPI_GELU_GRAD (no transposes). Split-K partials go to `fixed` (at most
+// fixed_floats floats) on any stream, or to leased scratch on the null stream
+// only. Returns false, launching nothing, for an unsupported combination.
+bool bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
+                 const float *B, float beta, float *C, hipStream_t stream, int epi,
+                 const float *bias, float *act, const float *pre, float *fixed,
+                 long long fixed_floats);
 
 }  // namespace bmb

@@ -346,18 +346,15 @@ bool gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
 
 void bmb::gemm_bias_nt(int M, int N, int K, const float *A, const float *W, const float *bias,
                        float *C, float *gelu_out) {
-    if (gelu_out != nullptr)
-        dispatch<false, true, bmb::EPI_BIAS_GELU>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0,
-                                                  nullptr, bmb::EpiArgs{bias, gelu_out, nullptr});
-    else
-        dispatch<false, true, bmb::EPI_BIAS>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0, nullptr,
-                                             bmb::EpiArgs{bias, nullptr, nullptr});
+    bmb::bf16x3_gemm(false, true, M, N, K, 1.0f, A, W, 0.0f, C, nullptr,
+                     gelu_out != nullptr ? bmb::EPI_BIAS_GELU : bmb::EPI_BIAS, bias, gelu_out,
+                     nullptr, nullptr, 0);
 }
 
 void bmb::gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B,
                             const float *pre, float *C) {
-    dispatch<false, false, bmb::EPI_GELU_GRAD>(1, M, N, K, 1.0f, A, 0, B, 0, 0.0f, C, 0, nullptr,
-                                               bmb::EpiArgs{nullptr, nullptr, pre});
+    bmb::bf16x3_gemm(false, false, M, N, K, 1.0f, A, B, 0.0f, C, nullptr, bmb::EPI_GELU_GRAD,
+                     nullptr, nullptr, pre, nullptr, 0);
 }
 
 void bmb::splitk_reduce(float *C, const float *P, int splits, long long mn, int N, float alpha,
@@ -366,12 +363,38 @@ void bmb::splitk_reduce(float *C, const float *P, int splits, long long mn, int 
                 dim3(256), 0, stream, C, P, splits, mn, N, alpha, beta, bmb::EpiArgs{});
 }
 
+void bmb::splitk_reduce_epi(int epi, float *C, const float *P, int splits, long long mn, int N,
+                            float alpha, float beta, hipStream_t stream, const float *bias,
+                            float *act, const float *pre) {
+    const dim3 grid((unsigned)((mn + 1023) / 1024)), block(256);
+    const bmb::EpiArgs ep{bias, act, pre};
+    switch (epi) {
+    case bmb::EPI_BIAS:
+        bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BIAS>, grid, block, 0, stream, C, P, splits,
+                    mn, N, alpha, beta, ep);
+        break;
+    case bmb::EPI_BIAS_GELU:
+        bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BIAS_GELU>, grid, block, 0, stream, C, P,
+                    splits, mn, N, alpha, beta, ep);
+        break;
+    case bmb::EPI_GELU_GRAD:
+        bmb::launch(bmb::splitk_reduce_k<bmb::EPI_GELU_GRAD>, grid, block, 0, stream, C, P,
+                    splits, mn, N, alpha, beta, ep);
+        break;
+    default:
+        bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BLAS>, grid, block, 0, stream, C, P, splits, mn,
+                    N, alpha, beta, ep);
+        break;
+    }
+}
+
 extern "C" {
 
 void gemm(bool transA, bool transB, int M, int N, int K, float alpha,
           const float *A, const float *B, float beta, float *C,
           hipStream_t stream) {
-    gemm_any(transA, transB, 1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream);
+    bmb::bf16x3_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream, bmb::EPI_BLAS,
+                     nullptr, nullptr, nullptr, nullptr, 0);
 }
 
 void batched_gemm(bool transA, bool transB, int batch, int M, int N, int K,
@@ -392,7 +415,9 @@ int gemm_noalloc(bool transA, bool transB, int M, int N, int K, float alpha, con
     if (M <= 0 || N <= 0) return 0;
     float *fixed = noalloc_scratch();
     if (fixed == nullptr) return -1;
-    return gemm_any(transA, transB, 1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, fixed)
+    return bmb::bf16x3_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream,
+                            bmb::EPI_BLAS, nullptr, nullptr, nullptr, fixed,
+                            NOALLOC_SPLIT_FLOATS)
                ? 0
                : -1;
 }

@@ -107,126 +107,140 @@ __device__ __forceinline__ void split4(const float (&x)[4], bf16x4 &hi, bf16x4 &
     }
 }
 
-template <class Tl, bool VEC>
-struct Bf16x3Gemm {
-    static constexpr int BM = Tl::BM, BN = Tl::BN, NT = Tl::NT;
-    static constexpr int FM = Tl::FM, FN = Tl::FN;
+// Staging of one operand's tile per stage: ROWS rows (m of A, n of B) x BK k,
+// into a hi and a lo plane. KCONT: k is the contiguous axis of the stored
+// operand (A not transposed, B transposed): 128-bit loads of four k, split,
+// one 64-bit store per plane. Otherwise rows are contiguous (A transposed, B
+// not): 4 x 4 blocks (four k rows of four consecutive m or n; a wave covers
+// 32 consecutive blocks of two k rows, so each load is two 512-byte coalesced
+// accesses), transposed in registers, one 64-bit store of four k per row and
+// plane.
+template <int ROWS, int NT, bool KCONT, bool VEC>
+struct OpStage {
+    static constexpr int CH = ROWS * BK / 4 / NT;      // KCONT: chunks per lane
+    static constexpr int BLK = BK * ROWS / 16;         // otherwise: 4 x 4 blocks per stage
+    static constexpr int PER_T = (BLK + NT - 1) / NT;  // blocks per lane
+    static constexpr int NLD = KCONT ? CH : 4 * PER_T;
+    static_assert(!KCONT || (ROWS * BK / 4) % NT == 0, "staging splits evenly over the lanes");
+    float4 v[NLD];
 
-    struct Regs {
-        float4 a[Tl::A_CH];
-        float4 b[Tl::B_PER_T][4];  // rows k..k+3 of a 4 x 4 block
-    };
-
-    // One 128-bit load from a 4-byte aligned address wholly inside the row.
+    __device__ static __forceinline__ bool skip(int j, int tid) {
+        return !KCONT && BLK % NT != 0 && tid + j * NT >= BLK;
+    }
+    // Chunk e (KCONT): row r, k c..c+3.
+    __device__ static __forceinline__ void chunk(int e, int &r, int &c) {
+        r = e / (BK / 4);
+        c = (e % (BK / 4)) * 4;
+    }
+    // Block e: k rows 4kb..4kb+3, rows rb..rb+3. Neighbouring lanes take the
+    // two halves of a 16-byte k chunk (kb even, odd) of one row block.
+    __device__ static __forceinline__ void block(int e, int &kb, int &rb) {
+        const int m = (e >> 1) % (ROWS / 4);
+        kb = 2 * ((e >> 1) / (ROWS / 4)) + (e & 1);
+        rb = 4 * m;
+    }
     __device__ static __forceinline__ float4 ld_in(const float *p) {
         if (VEC) return bmb::ld4(p);
-        float4 v;
-        __builtin_memcpy(&v, p, sizeof(v));
-        return v;
+        float4 x;
+        __builtin_memcpy(&x, p, sizeof(x));
+        return x;
     }
-
-    // Stage loads with zero fill outside [0, M) x [0, K) of A and
-    // [0, K) x [0, N) of B (K is the range's length; lda = full K, ldb = N).
-    __device__ static __forceinline__ void load_guarded(Regs &g, const float *A, const float *B,
-                                                        int M, int N, int K, int lda, int ldb,
-                                                        int m0, int n0, int k0, int tid) {
+    // Byte offsets of this lane's loads from the stage base (row 0, k 0 of the
+    // tile): loop-invariant and 32-bit.
+    __device__ static __forceinline__ void offsets(unsigned (&o)[NLD], int ld, int tid) {
+        if (KCONT) {
 #pragma unroll
-        for (int i = 0; i < Tl::A_CH; ++i) {
-            const int e = tid + i * NT, r = e / (BK / 4), c = (e % (BK / 4)) * 4;
-            g.a[i] = bmb::load_chunk<VEC>(A, M, K, lda, m0 + r, k0 + c);
-        }
+            for (int i = 0; i < NLD; ++i) {
+                int r, c;
+                chunk(tid + i * NT, r, c);
+                o[i] = 4u * ((unsigned)r * (unsigned)ld + (unsigned)c);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < Tl::B_PER_T; ++j) {
-            const int e = tid + j * NT;
-            if (Tl::B_BLK % NT != 0 && e >= Tl::B_BLK) continue;
-            int kb, nb;
-            b_block(e, kb, nb);
+            for (int j = 0; j < PER_T; ++j) {
+                int kb, rb;
+                block(min(tid + j * NT, BLK - 1), kb, rb);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                g.b[j][i] = bmb::load_chunk<VEC>(B, K, N, ldb, k0 + 4 * kb + i, n0 + nb);
-        }
-    }
-
-    // Byte offsets of this lane's chunks from the tile's stage base (A at
-    // (m0, k0), B at (k0, n0)): loop-invariant and 32-bit, so an interior
-    // stage's loads take a uniform base and no 64-bit address arithmetic.
-    struct Offs {
-        unsigned a[Tl::A_CH];
-        unsigned b[Tl::B_PER_T][4];
-    };
-    __device__ static __forceinline__ void offsets(Offs &o, int lda, int ldb, int tid) {
-#pragma unroll
-        for (int i = 0; i < Tl::A_CH; ++i) {
-            const int e = tid + i * NT, r = e / (BK / 4), c = (e % (BK / 4)) * 4;
-            o.a[i] = 4u * ((unsigned)r * (unsigned)lda + (unsigned)c);
-        }
-#pragma unroll
-        for (int j = 0; j < Tl::B_PER_T; ++j) {
-            const int e = min(tid + j * NT, Tl::B_BLK - 1);
-            int kb, nb;
-            b_block(e, kb, nb);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                o.b[j][i] = 4u * ((unsigned)(4 * kb + i) * (unsigned)ldb + (unsigned)nb);
-        }
-    }
-    __device__ static __forceinline__ float4 ld_at(const float *base, unsigned off) {
-        return ld_in(reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + off));
-    }
-    // Interior stage: every chunk inside the operands.
-    __device__ static __forceinline__ void load_interior(Regs &g, const Offs &o, const float *a0,
-                                                         const float *b0, int tid) {
-#pragma unroll
-        for (int i = 0; i < Tl::A_CH; ++i) g.a[i] = ld_at(a0, o.a[i]);
-#pragma unroll
-        for (int j = 0; j < Tl::B_PER_T; ++j) {
-            if (Tl::B_BLK % NT != 0 && tid + j * NT >= Tl::B_BLK) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) g.b[j][i] = ld_at(b0, o.b[j][i]);
-        }
-    }
-
-    // 4 x 4 block e of B: k rows 4kb..4kb+3 and columns nb..nb+3 of the stage.
-    // Neighbouring lanes take the two halves of a 16-byte k chunk (kb even,
-    // odd) of one column block; pairs of lanes walk the column blocks.
-    __device__ static __forceinline__ void b_block(int e, int &kb, int &nb) {
-        const int m = (e >> 1) % (BN / 4);
-        kb = 2 * ((e >> 1) / (BN / 4)) + (e & 1);
-        nb = 4 * m;
-    }
-
-    // Split the prefetched stage into the four planes of `st`.
-    __device__ static __forceinline__ void store(const Regs &g, __bf16 *st, int tid) {
-#pragma unroll
-        for (int i = 0; i < Tl::A_CH; ++i) {
-            const int e = tid + i * NT, r = e / (BK / 4), c = (e % (BK / 4)) * 4;
-            const float x[4] = {g.a[i].x, g.a[i].y, g.a[i].z, g.a[i].w};
-            bf16x4 h, l;
-            split4(x, h, l);
-            *reinterpret_cast<bf16x4 *>(st + lds_off(r, c)) = h;
-            *reinterpret_cast<bf16x4 *>(st + Tl::A_PLANE + lds_off(r, c)) = l;
-        }
-        __bf16 *bh = st + 2 * Tl::A_PLANE, *bl = bh + Tl::B_PLANE;
-#pragma unroll
-        for (int j = 0; j < Tl::B_PER_T; ++j) {
-            const int e = tid + j * NT;
-            if (Tl::B_BLK % NT != 0 && e >= Tl::B_BLK) continue;
-            int kb, nb;
-            b_block(e, kb, nb);
-            const float4 *b = g.b[j];
-            const float cols[4][4] = {{b[0].x, b[1].x, b[2].x, b[3].x},
-                                      {b[0].y, b[1].y, b[2].y, b[3].y},
-                                      {b[0].z, b[1].z, b[2].z, b[3].z},
-                                      {b[0].w, b[1].w, b[2].w, b[3].w}};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                bf16x4 h, l;
-                split4(cols[c], h, l);
-                *reinterpret_cast<bf16x4 *>(bh + lds_off(nb + c, 4 * kb)) = h;
-                *reinterpret_cast<bf16x4 *>(bl + lds_off(nb + c, 4 * kb)) = l;
+                for (int i = 0; i < 4; ++i)
+                    o[4 * j + i] = 4u * ((unsigned)(4 * kb + i) * (unsigned)ld + (unsigned)rb);
             }
         }
     }
+    // Interior stage: base = the stage's (row 0, k 0) element.
+    __device__ __forceinline__ void load_interior(const float *base, const unsigned (&o)[NLD],
+                                                  int tid) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            if (skip(i / 4, tid)) continue;
+            v[i] = ld_in(reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + o[i]));
+        }
+    }
+    // Zero fill outside the operand: P is the K range's origin, R its rows
+    // (M or N), K the range's length, ld the stored row stride.
+    __device__ __forceinline__ void load_guarded(const float *P, int R, int K, int ld, int r0,
+                                                 int k0, int tid) {
+        if (KCONT) {
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                int r, c;
+                chunk(tid + i * NT, r, c);
+                v[i] = bmb::load_chunk<VEC>(P, R, K, ld, r0 + r, k0 + c);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER_T; ++j) {
+                if (skip(j, tid)) continue;
+                int kb, rb;
+                block(tid + j * NT, kb, rb);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[4 * j + i] = bmb::load_chunk<VEC>(P, K, R, ld, k0 + 4 * kb + i, r0 + rb);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(__bf16 *hi, __bf16 *lo, int tid) const {
+        if (KCONT) {
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                int r, c;
+                chunk(tid + i * NT, r, c);
+                const float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+                bf16x4 h, l;
+                split4(x, h, l);
+                *reinterpret_cast<bf16x4 *>(hi + lds_off(r, c)) = h;
+                *reinterpret_cast<bf16x4 *>(lo + lds_off(r, c)) = l;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER_T; ++j) {
+                if (skip(j, tid)) continue;
+                int kb, rb;
+                block(tid + j * NT, kb, rb);
+                const float4 *b = v + 4 * j;
+                const float cols[4][4] = {{b[0].x, b[1].x, b[2].x, b[3].x},
+                                          {b[0].y, b[1].y, b[2].y, b[3].y},
+                                          {b[0].z, b[1].z, b[2].z, b[3].z},
+                                          {b[0].w, b[1].w, b[2].w, b[3].w}};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    bf16x4 h, l;
+                    split4(cols[c], h, l);
+                    *reinterpret_cast<bf16x4 *>(hi + lds_off(rb + c, 4 * kb)) = h;
+                    *reinterpret_cast<bf16x4 *>(lo + lds_off(rb + c, 4 * kb)) = l;
+                }
+            }
+        }
+    }
+};
+
+// op(A) is M x K, op(B) K x N; stored A is M x K (lda = K) or, TA, K x M
+// (lda = M); stored B is K x N (ldb = N) or, TB, N x K (ldb = K). C is M x N.
+template <class Tl, bool TA, bool TB, bool VEC>
+struct Bf16x3Gemm {
+    static constexpr int BM = Tl::BM, BN = Tl::BN, NT = Tl::NT;
+    static constexpr int FM = Tl::FM, FN = Tl::FN;
+    using SA = OpStage<BM, NT, !TA, VEC>;
+    using SB = OpStage<BN, NT, TB, VEC>;
 
     // One 16-k step of MFMAs on stage `st`: for every 32 x 32 block,
     // acc += lo_a hi_b, then hi_a lo_b, then hi_a hi_b (small terms first).
@@ -258,13 +272,14 @@ struct Bf16x3Gemm {
 
     // One output tile over k in [0, K) (A, B positioned at that range's
     // start). INTERIOR: the tile lies inside M x N and K is a positive whole
-    // number of stages, so no load or store needs a bounds check. PARTIAL:
-    // C receives the raw sums (a split-K partial, row stride N).
-    template <bool INTERIOR, bool PARTIAL>
+    // number of stages, so no load or store needs a bounds check. EPI: what
+    // the epilogue stores (bmb::Epi; EPI_PARTIAL: the raw sums, row stride N).
+    template <bool INTERIOR, int EPI>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb, float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B, float beta, float *C,
-                                               int m0, int n0, __bf16 *smem) {
+                                               int m0, int n0, __bf16 *smem,
+                                               const bmb::EpiArgs &ep) {
         const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tl::WAVES_N) * Tl::WM, wn = (wave % Tl::WAVES_N) * Tl::WN;
 
@@ -277,19 +292,36 @@ struct Bf16x3Gemm {
                 for (int r = 0; r < 16; ++r) acc[fi][fn][r] = 0.0f;
 
         const int nkt = (K + BK - 1) / BK;
-        Regs g;
-        Offs o;
-        if (INTERIOR) offsets(o, lda, ldb, tid);
-        // Stage kt's tile bases (uniform): A at (m0, kt*BK), B at (kt*BK, n0).
-        auto a_at = [&](int kt) { return A + (size_t)m0 * lda + (size_t)kt * BK; };
-        auto b_at = [&](int kt) { return B + (size_t)kt * BK * ldb + n0; };
+        SA ga;
+        SB gb;
+        unsigned oa[SA::NLD], ob[SB::NLD];
+        if (INTERIOR) {
+            SA::offsets(oa, lda, tid);
+            SB::offsets(ob, ldb, tid);
+        }
+        // Stage kt's bases (uniform): the (row 0, k 0) element of each tile.
+        auto a_at = [&](int kt) {
+            return TA ? A + (size_t)kt * BK * lda + m0 : A + (size_t)m0 * lda + (size_t)kt * BK;
+        };
+        auto b_at = [&](int kt) {
+            return TB ? B + (size_t)n0 * ldb + (size_t)kt * BK : B + (size_t)kt * BK * ldb + n0;
+        };
         auto load = [&](int kt) {
-            if (INTERIOR) load_interior(g, o, a_at(kt), b_at(kt), tid);
-            else load_guarded(g, A, B, M, N, K, lda, ldb, m0, n0, kt * BK, tid);
+            if (INTERIOR) {
+                ga.load_interior(a_at(kt), oa, tid);
+                gb.load_interior(b_at(kt), ob, tid);
+            } else {
+                ga.load_guarded(A, M, K, lda, m0, kt * BK, tid);
+                gb.load_guarded(B, N, K, ldb, n0, kt * BK, tid);
+            }
+        };
+        auto store = [&](__bf16 *st) {
+            ga.store(st, st + Tl::A_PLANE, tid);
+            gb.store(st + 2 * Tl::A_PLANE, st + 2 * Tl::A_PLANE + Tl::B_PLANE, tid);
         };
         if (nkt > 0) {
             load(0);
-            store(g, smem, tid);
+            store(smem);
             if (nkt > 1) load(1);
         }
         __syncthreads();
@@ -298,7 +330,7 @@ struct Bf16x3Gemm {
             step(st, 0, wm, wn, lane, acc);
             if (kt + 1 < nkt) {
                 // The other stage was last read before the previous barrier.
-                store(g, smem + ((kt + 1) & 1) * Tl::STAGE, tid);
+                store(smem + ((kt + 1) & 1) * Tl::STAGE);
                 if (kt + 2 < nkt) load(kt + 2);
             }
             step(st, 1, wm, wn, lane, acc);
@@ -306,14 +338,23 @@ struct Bf16x3Gemm {
         }
 
         // Epilogue: lanes 0-31 of a register cover 32 consecutive columns.
-        // The C values a row of FN blocks needs (beta != 0) are gathered
-        // before any result is stored: 16 * FN loads in flight per lane.
+        // Whatever a row of FN blocks reads (C for beta != 0, the GELU input)
+        // is gathered before any result is stored: 16 * FN loads in flight.
         const int l32 = lane & 31, half = lane >> 5;
-        const bool reads = !PARTIAL && beta != 0.0f;
+        const bool reads = (EPI == bmb::EPI_BLAS && beta != 0.0f) || EPI == bmb::EPI_GELU_GRAD;
+        float bias[FN];
+        if (EPI == bmb::EPI_BIAS || EPI == bmb::EPI_BIAS_GELU) {
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+                const int col = n0 + wn + fn * 32 + l32;
+                bias[fn] = (INTERIOR || col < N) ? ep.bias[col] : 0.0f;
+            }
+        }
 #pragma unroll
         for (int fi = 0; fi < FM; ++fi) {
             float in[FN][16];
             if (reads) {
+                const float *src = EPI == bmb::EPI_GELU_GRAD ? ep.pre : C;
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn) {
                     const int col = n0 + wn + fn * 32 + l32;
@@ -321,7 +362,7 @@ struct Bf16x3Gemm {
                     for (int r = 0; r < 16; ++r) {
                         const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                         in[fn][r] = (INTERIOR || (row < M && col < N))
-                                        ? C[(size_t)row * N + col] : 0.0f;
+                                        ? src[(size_t)row * N + col] : 0.0f;
                     }
                 }
             }
@@ -334,8 +375,18 @@ struct Bf16x3Gemm {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (!INTERIOR && row >= M) continue;
                     const float a = acc[fi][fn][r];
-                    C[(size_t)row * N + col] =
-                        PARTIAL ? a : (reads ? bmb::fma_rn(alpha, a, beta * in[fn][r]) : alpha * a);
+                    const size_t idx = (size_t)row * N + col;
+                    if (EPI == bmb::EPI_PARTIAL) {
+                        C[idx] = a;
+                    } else if (EPI == bmb::EPI_BLAS) {
+                        C[idx] = reads ? bmb::fma_rn(alpha, a, beta * in[fn][r]) : alpha * a;
+                    } else if (EPI == bmb::EPI_GELU_GRAD) {
+                        C[idx] = bmb::gelu_grad(in[fn][r], a);
+                    } else {
+                        const float v = a + bias[fn];
+                        C[idx] = v;
+                        if (EPI == bmb::EPI_BIAS_GELU) ep.act[idx] = bmb::gelu(v);
+                    }
                 }
             }
         }
@@ -344,25 +395,27 @@ struct Bf16x3Gemm {
 
 // Grid: x = output tiles (XCD-remapped, grouped), y = K range s, covering
 // k in [s*kchunk, min(K, (s+1)*kchunk)) (kchunk a multiple of BK when
-// gridDim.y > 1). PARTIAL: write the range's raw sums to C + s*M*N.
-template <class Tl, bool VEC, bool PARTIAL>
+// gridDim.y > 1). EPI_PARTIAL: write the range's raw sums to C + s*M*N.
+template <class Tl, bool TA, bool TB, bool VEC, int EPI>
 __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchunk, float alpha,
                                                    const float *__restrict__ A,
                                                    const float *__restrict__ B, float beta,
-                                                   float *C, int tiles_m, int tiles_n) {
+                                                   float *C, int tiles_m, int tiles_n,
+                                                   bmb::EpiArgs ep) {
     extern __shared__ __bf16 lds[];
-    using G = Bf16x3Gemm<Tl, VEC>;
+    using G = Bf16x3Gemm<Tl, TA, TB, VEC>;
     int tm, tn;
     bmb::group_tile(bmb::xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const int m0 = tm * Tl::BM, n0 = tn * Tl::BN;
+    const int lda = TA ? M : K, ldb = TB ? K : N;
     const int kb = blockIdx.y * kchunk, klen = min(K, kb + kchunk) - kb;
-    const float *Ak = A + kb;
-    const float *Bk = B + (size_t)kb * N;
-    float *Cs = PARTIAL ? C + (size_t)blockIdx.y * M * N : C;
+    const float *Ak = TA ? A + (size_t)kb * lda : A + kb;
+    const float *Bk = TB ? B + kb : B + (size_t)kb * ldb;
+    float *Cs = EPI == bmb::EPI_PARTIAL ? C + (size_t)blockIdx.y * M * N : C;
     if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0 && klen % BK == 0)
-        G::template run<true, PARTIAL>(M, N, klen, K, N, alpha, Ak, Bk, beta, Cs, m0, n0, lds);
+        G::template run<true, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, m0, n0, lds, ep);
     else
-        G::template run<false, PARTIAL>(M, N, klen, K, N, alpha, Ak, Bk, beta, Cs, m0, n0, lds);
+        G::template run<false, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, m0, n0, lds, ep);
 }
 
 // ------------------------------------------------------------- host side
@@ -394,9 +447,10 @@ constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;  // 256 MiB of partials
 template <class Tl>
 int occupancy_of() {
     int n = 0;
-    bmb::allow_smem(bf16x3_k<Tl, true, false>, Tl::SMEM_BYTES);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bf16x3_k<Tl, true, false>, Tl::NT,
-                                                     Tl::SMEM_BYTES) != hipSuccess) {
+    auto kern = bf16x3_k<Tl, false, false, true, bmb::EPI_BLAS>;
+    bmb::allow_smem(kern, Tl::SMEM_BYTES);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, Tl::NT, Tl::SMEM_BYTES) !=
+        hipSuccess) {
         (void)hipGetLastError();
         n = 1;
     }
@@ -407,7 +461,9 @@ struct Plan {
     int tile, splits, kchunk;
 };
 
-Plan pick(int M, int N, int K) {
+// may_split: split-K partials have somewhere to go; max_floats caps them
+// (splits * M * N).
+Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
     static std::once_flag once[64];
     static int occ[64][N_CANDS], cus[64];
     int dev = 0;
@@ -432,12 +488,12 @@ Plan pick(int M, int N, int K) {
         for (int s : SPLITS) {
             int splits = 1, kchunk = K;
             if (s > 1) {
-                if (K < 2 * MIN_SPLIT_K) continue;
+                if (!may_split || K < 2 * MIN_SPLIT_K) continue;
                 kchunk = (K + s - 1) / s;
                 kchunk = (kchunk + BK - 1) / BK * BK;
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
-                if (splits < 2 || (long long)splits * M * N > MAX_SPLIT_FLOATS) continue;
+                if (splits < 2 || (long long)splits * M * N > max_floats) continue;
             }
             const long long items = tiles * splits;
             const long long slots = (long long)cus[dev] * occ[dev][t];
@@ -464,48 +520,96 @@ Plan pick(int M, int N, int K) {
     return best;
 }
 
-template <class Tl, bool VEC, bool PARTIAL>
+template <class Tl, bool TA, bool TB, int EPI>
 void launch(int M, int N, int K, int kchunk, int splits, float alpha, const float *A,
-            const float *B, float beta, float *C) {
-    auto kern = bf16x3_k<Tl, VEC, PARTIAL>;
-    bmb::allow_smem(kern, Tl::SMEM_BYTES);
+            const float *B, float beta, float *C, bool vec, hipStream_t stream,
+            bmb::EpiArgs ep) {
     const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
-    bmb::launch(kern, dim3(tiles_m * tiles_n, splits), dim3(Tl::NT), Tl::SMEM_BYTES, nullptr, M,
-                N, K, kchunk, alpha, A, B, beta, C, tiles_m, tiles_n);
+    const dim3 grid(tiles_m * tiles_n, splits);
+    if (vec) {
+        auto kern = bf16x3_k<Tl, TA, TB, true, EPI>;
+        bmb::allow_smem(kern, Tl::SMEM_BYTES);
+        bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
+                    B, beta, C, tiles_m, tiles_n, ep);
+    } else {
+        auto kern = bf16x3_k<Tl, TA, TB, false, EPI>;
+        bmb::allow_smem(kern, Tl::SMEM_BYTES);
+        bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
+                    B, beta, C, tiles_m, tiles_n, ep);
+    }
 }
 
-template <class Tl>
+// A plan on tile Tl: one launch with the epilogue, or the split partials
+// (EPI_PARTIAL into P) and the shared reduce with the epilogue.
+template <class Tl, bool TA, bool TB, int EPI>
 void run_plan(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
-              float beta, float *C, bool vec, float *P) {
-    if (P != nullptr) {
-        if (vec) launch<Tl, true, true>(M, N, K, p.kchunk, p.splits, 1.0f, A, B, 0.0f, P);
-        else     launch<Tl, false, true>(M, N, K, p.kchunk, p.splits, 1.0f, A, B, 0.0f, P);
-        bmb::splitk_reduce(C, P, p.splits, (long long)M * N, N, alpha, beta, nullptr);
+              float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
+    if (p.splits > 1) {
+        launch<Tl, TA, TB, bmb::EPI_PARTIAL>(M, N, K, p.kchunk, p.splits, 1.0f, A, B, 0.0f, P, vec,
+                                             stream, ep);
+        bmb::splitk_reduce_epi(EPI, C, P, p.splits, (long long)M * N, N, alpha, beta, stream,
+                               ep.bias, ep.act, ep.pre);
     } else {
-        if (vec) launch<Tl, true, false>(M, N, K, K, 1, alpha, A, B, beta, C);
-        else     launch<Tl, false, false>(M, N, K, K, 1, alpha, A, B, beta, C);
+        launch<Tl, TA, TB, EPI>(M, N, K, K, 1, alpha, A, B, beta, C, vec, stream, ep);
+    }
+}
+
+template <bool TA, bool TB, int EPI>
+void run_tiles(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
+               float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
+    switch (p.tile) {
+    case 0: run_plan<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
+    case 1: run_plan<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
+    default: run_plan<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
     }
 }
 
 }  // namespace
 
+// The bf16x3 GEMM behind gemm(), gemm_noalloc() and the GPT's fused linear
+// layers (gemm_fused.hpp). Split-K partials go to `fixed` (at most
+// fixed_floats) on any stream, or else to leased scratch, used only on the null
+// stream (its reuse is ordered by the null stream). The epilogue is one of
+// EPI_BLAS (any transposes), EPI_BIAS / EPI_BIAS_GELU (A @ W^T) and
+// EPI_GELU_GRAD (A @ B). Returns false, with nothing launched, for another
+// combination.
+bool bmb::bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
+                      const float *B, float beta, float *C, hipStream_t stream, int epi,
+                      const float *bias, float *act, const float *pre, float *fixed,
+                      long long fixed_floats) {
+    if (M <= 0 || N <= 0) return true;
+    const bmb::EpiArgs ep{bias, act, pre};
+    const int a_contig = ta ? M : K, b_contig = tb ? K : N;
+    const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && (((uintptr_t)A & 15) == 0) &&
+                     (((uintptr_t)B & 15) == 0);
+    const bool may_split = fixed != nullptr || stream == nullptr;
+    Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
+    float *P = fixed;
+    std::optional<bmb::ScratchLease> lease;
+    if (p.splits > 1 && fixed == nullptr) {
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
+        P = static_cast<float *>(lease->get());
+        if (P == nullptr) p = pick(M, N, K, false, 0);  // no scratch: no split
+    }
+#define BMB_B3(TA_, TB_, EPI_)                                                              \
+    run_tiles<TA_, TB_, EPI_>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep);        \
+    return true;
+    if (epi == bmb::EPI_BLAS) {
+        if (!ta && !tb) { BMB_B3(false, false, bmb::EPI_BLAS) }
+        if (!ta && tb) { BMB_B3(false, true, bmb::EPI_BLAS) }
+        if (ta && !tb) { BMB_B3(true, false, bmb::EPI_BLAS) }
+        BMB_B3(true, true, bmb::EPI_BLAS)
+    }
+    if (epi == bmb::EPI_BIAS && !ta && tb) { BMB_B3(false, true, bmb::EPI_BIAS) }
+    if (epi == bmb::EPI_BIAS_GELU && !ta && tb) { BMB_B3(false, true, bmb::EPI_BIAS_GELU) }
+    if (epi == bmb::EPI_GELU_GRAD && !ta && !tb) { BMB_B3(false, false, bmb::EPI_GELU_GRAD) }
+#undef BMB_B3
+    return false;
+}
+
 extern "C" void sgemm_mfma_bf16x3(int M, int N, int K, float alpha,
                                   const float *A, const float *B, float beta,
                                   float *C) {
-    if (M <= 0 || N <= 0) return;
-    const bool vec = K % 4 == 0 && N % 4 == 0 && (((uintptr_t)A & 15) == 0) &&
-                     (((uintptr_t)B & 15) == 0);
-    Plan p = pick(M, N, K);
-    float *P = nullptr;
-    std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1) {
-        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
-        P = static_cast<float *>(lease->get());
-        if (P == nullptr) p = Plan{p.tile, 1, K};  // no scratch: no split
-    }
-    switch (p.tile) {
-    case 0: run_plan<TileL>(p, M, N, K, alpha, A, B, beta, C, vec, P); break;
-    case 1: run_plan<TileM>(p, M, N, K, alpha, A, B, beta, C, vec, P); break;
-    default: run_plan<TileS>(p, M, N, K, alpha, A, B, beta, C, vec, P); break;
-    }
+    bmb::bf16x3_gemm(false, false, M, N, K, alpha, A, B, beta, C, nullptr, bmb::EPI_BLAS,
+                     nullptr, nullptr, nullptr, nullptr, 0);
 }

@@ -23,6 +23,20 @@ def fp32_order_bound(K):
     return 4.0 * np.sqrt(max(K, 1)) * u + 4.0 * u
 
 
+def bf16x3_err(got, ta, tb, M, N, K, alpha, A, B, beta, C0):
+    """Normwise error of gemm()'s result against the exact value of its
+    bf16x3 split (oracle.gemm_bf16x3_f64: three exact bf16 x bf16 products per
+    term), with the bound it is held to: fp32 summation of 3K terms
+    (fp32_order_bound(3K)). A dropped or doubled cross term, or a truncating
+    split, misses it by orders of magnitude."""
+    import oracle as O
+    Aop = np.ascontiguousarray(A.reshape(K, M).T if ta else A.reshape(M, K))
+    Bop = np.ascontiguousarray(B.reshape(N, K).T if tb else B.reshape(K, N))
+    want = O.gemm_bf16x3_f64(M, N, K, alpha, Aop, Bop, beta, C0)
+    err, bad = O.normwise(np.asarray(got).reshape(M, N), want)
+    return (err if bad == 0 else float("inf")), fp32_order_bound(3 * K)
+
+
 def dev(a):
     """Host numpy array -> device float32 tensor (contiguous copy)."""
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda")

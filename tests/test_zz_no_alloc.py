@@ -7,7 +7,8 @@ cannot call hipMalloc (graph capture, serving loops). Through the C-ABI:
     bit (both split K the same way: these partials fit the array), on the
     null stream and on a non-null stream, where gemm() itself does not split
     (so the bits differ from gemm() there: the variant did split);
-  * each is within the fp32 summation-order bound of the fp64 oracle;
+  * each is within the bf16x3 summation bound of the split's exact value
+    (gemm() runs on bf16x3 products);
   * the device's free memory is the same before and after the calls.
 """
 import numpy as np
@@ -15,7 +16,7 @@ import pytest
 
 import bmb
 import oracle as O
-from gpu_util import fp32_order_bound
+from gpu_util import bf16x3_err
 
 pytestmark = pytest.mark.gpu
 
@@ -54,7 +55,7 @@ def test_noalloc_matches_gemm(gpu):
         side.synchronize()
         d["nosplit"] = _bits(d["C"])
         bmb.check("gemm references")
-        d["oracle"] = O.gemm_f64(ta, tb, M, N, K, 0.75, A, B, 1.25, C0)
+        d["host"] = (A, B, C0)
         data.append(d)
     torch.cuda.synchronize()
     free0 = torch.cuda.mem_get_info()[0]
@@ -75,8 +76,9 @@ def test_noalloc_matches_gemm(gpu):
             got = _bits(d["C"])
             assert np.array_equal(got, d["ref"])
             assert not np.array_equal(got, d["nosplit"])
-            err, bad = O.normwise(got.view(np.float32), d["oracle"])
-            assert bad == 0 and err < fp32_order_bound(K), err
+            A, B, C0 = d["host"]
+            err, bound = bf16x3_err(got.view(np.float32), ta, tb, M, N, K, 0.75, A, B, 1.25, C0)
+            assert err < bound, (err, bound)
     torch.cuda.synchronize()
     free1 = torch.cuda.mem_get_info()[0]
     print("free memory before %.1f MiB, after %.1f MiB" % (free0 / 2**20, free1 / 2**20))
