@@ -9,9 +9,14 @@
  *     op(B) = B   with B stored K x N (ldb = N)   when transB == false
  *           = B^T with B stored N x K (ldb = K)   when transB == true
  * Pointers are caller-owned device pointers. beta == 0 means C is write-only.
- * Computation is fp32 in, fp32 products, fp32 accumulation on MFMA matrix
- * cores; normwise error against an exact reference is at fp32 rounding level
- * (held to 1e-4, the reference's bar, tools/test_gemm.cu:107).
+ * gemm() (and gemm_noalloc()) computes on bf16x3 matrix-core products: each
+ * fp32 operand is split into bfloat16 hi + lo (x - hi is exact in fp32),
+ * every product term is hi*hi + hi*lo + lo*hi (each bf16 x bf16 product exact
+ * in fp32) and accumulation is fp32. What is dropped (lo*lo and the rounding
+ * of lo) is a few 2^-17 of |a b| per product, so the normwise error against
+ * the exact product is ~1e-6, a hundred times inside the reference's 1e-4 bar
+ * (tools/test_gemm.cu:107). batched_gemm() uses fp32 matrix-core products
+ * (fp32 rounding level).
  */
 #ifndef BMB_GEMM_H
 #define BMB_GEMM_H
