@@ -1905,7 +1905,6 @@ __device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ d
 
     for (int t = 0; t < nqt; ++t) {
         const int qb = (tq0 + t) * 32;
-        load_tile(t + 1);
         const float4 m_after = tile_max(t + 2);
         if (active && qb >= k0w) {
             const char *buf = smem + (t & 1) * S::KV_BUF;
@@ -1928,7 +1927,10 @@ __device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ d
                                      qb, key, T, l32, hf, dso);
         }
         // Stage tile t+1 (past the last tile: the last again, into the buffer
-        // nobody reads).
+        // nobody reads). Its loads are issued only now: held across the tile's
+        // work their registers would push the kernel past 256 VGPRs, and the
+        // other workgroup's wave on the SIMD covers their latency.
+        load_tile(t + 1);
         qo.store(smem + ((t + 1) & 1) * S::KV_BUF, max_exp(m_next.x), max_exp(m_next.y), tid);
         m_cur = m_next;
         m_next = m_after;
