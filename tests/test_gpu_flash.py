@@ -160,6 +160,57 @@ def test_forward_input_range(gpu, kind):
         assert bad == 0 and eo < TOL and el < 1e-5, (kind, cfg, eo, el)
 
 
+def _bwd_range_inputs(kind, B, T, C):
+    """(qkv, dout) whose magnitudes leave fp16's range while the attention
+    stays as well conditioned as at unit scale, so an fp32 backward meets the
+    same bar: scores are kept unchanged (Q scaled up exactly as K is scaled
+    down), or whole tensors are scaled (every gradient scales with them), or
+    single 32-row tiles of V and dO are scaled up, down or zeroed, which
+    moves the per-tile and running exponents of the backward mid-sequence."""
+    qkv = O.fill_xorshift(B * T * 3 * C, 1234).reshape(B, T, 3 * C).astype(np.float64)
+    dout = O.fill_xorshift(B * T * C, 99).reshape(B, T, C).astype(np.float64)
+    q, k, v = qkv[:, :, :C], qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
+    if kind == "qk_skew":
+        q *= 2.0 ** 20
+        k *= 2.0 ** -20
+    elif kind == "v_big":
+        v *= 1e20
+    elif kind == "dout_tiny":
+        dout *= 1e-30
+    elif kind == "tiles":
+        v[:, 100:130] *= 2.0 ** 40   # loud values late: the running exponents move
+        v[:, 10:20] *= 2.0 ** -40    # quiet values inside a tile
+        v[:, 140:180] = 0.0          # zero values
+        dout[:, 64:96] *= 2.0 ** 30  # one tile of loud output gradients
+        dout[:, 200:232] = 0.0       # a tile of zero output gradients
+        q[:, 5:9] *= 2.0 ** -30      # quiet queries
+    return qkv.astype(np.float32), dout.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["qk_skew", "v_big", "dout_tiny", "tiles"])
+def test_backward_input_range(gpu, kind):
+    """Every backward config against the fp64 oracle on the inputs of
+    _bwd_range_inputs, dq, dk and dv each held to the reference's normwise
+    1e-5 (and dsum to 1e-5 of its largest magnitude)."""
+    B, T, C, NH = 2, 257, 256, 4
+    qkv, dout = _bwd_range_inputs(kind, B, T, C)
+    d_qkv, out, lse = _run_fwd(qkv, B, T, C, NH)
+    ref_d = O.attn_bwd_f64(qkv, dout, B, T, C, NH)
+    ref_ds = O.dsum_f64(dout, out.get().reshape(B, T, C), B, T, C, NH)
+    for cfg in range(len(bmb.flash_bwd_configs())):
+        dq, ds = _run_bwd(d_qkv, out, lse, dout, B, T, C, NH, cfg)
+        # Plain per-slice normwise: no slice is zero in exact arithmetic here,
+        # and scaling makes some far smaller than the others on purpose.
+        errs = []
+        for s in range(3):
+            e, bad = O.normwise(dq[:, :, s * C:(s + 1) * C], ref_d[:, :, s * C:(s + 1) * C])
+            errs.append(e if bad == 0 else float("inf"))
+        eq, ek, ev = errs
+        ed = np.abs(ds - ref_ds).max() / max(np.abs(ref_ds).max(), 1e-300)
+        print("%s bwd cfg %d: dq %.2e dk %.2e dv %.2e dsum %.2e" % (kind, cfg, eq, ek, ev, ed))
+        assert eq < TOL and ek < TOL and ev < TOL and ed < 1e-5, (kind, cfg, eq, ek, ev, ed)
+
+
 @pytest.mark.parametrize("cfg", range(MAX_CFGS))
 def test_every_backward_config(gpu, cfg):
     if cfg >= len(bmb.flash_bwd_configs()):
