@@ -16,9 +16,10 @@
 // instructions are FMAs, a third of them issued on the second port.
 //
 // Structure.
-//   * 256 lanes = 4 wave64 per workgroup; tiles of 128 x 128, 64 x 128 and
-//     64 x 64 outputs, chosen per shape (pick_tile): the small tiles fill the
-//     device when M x N is small, the large one reads less LDS per FMA.
+//   * 256 lanes = 4 wave64 per workgroup; tiles of 128 x 128, 64 x 128,
+//     64 x 64 and 64 x 32 outputs, chosen per shape (pick_tile): the small
+//     tiles fill the device when M x N is small, the large one reads less LDS
+//     per FMA.
 //   * Each wave owns a quarter of the tile; each lane a patch of 4 x 4 strips
 //     (two 4-row strips 32 rows apart and two 4-column strips 32 columns
 //     apart in the 128 x 128 tile). The 8 lanes sharing a strip row read one
@@ -49,19 +50,21 @@ namespace {
 constexpr int NT = 256;
 constexpr int APAD = 4;
 
-// Tile of 64*TMS x 64*TNS outputs for 4 waves (2 x 2), each wave a
-// 32*TMS x 32*TNS quadrant; each lane a patch of TMS x TNS strips of 4 x 4
-// outputs, strips 32 rows / columns apart, so the 8 lanes sharing a strip row
-// (or column) read one float4 each of a 32-float LDS span per k: every LDS
-// read is conflict-free and 128-bit. 128 x 128 (TMS = TNS = 2) keeps 64
-// accumulators per lane and reads 1 byte of LDS per FMA; 64 x 64 (1, 1) has 4x
-// the workgroups for a small C at 2 bytes per FMA.
-template <int TMS_, int TNS_, int BK_, int UNROLL_>
+// Tile of 64*TMS x 16*SW*TNS outputs for 4 waves (2 x 2), each wave a
+// 32*TMS x 8*SW*TNS quadrant; each lane a patch of TMS x TNS strips of
+// 4 x SW outputs, strips 32 rows / 8*SW columns apart, so the 8 lanes sharing
+// a strip row (or column) read one float4 (float2) each of a contiguous LDS
+// span per k: every LDS read is conflict-free and 128-bit (64-bit for SW = 2).
+// 128 x 128 (TMS = TNS = 2, SW = 4) keeps 64 accumulators per lane and reads
+// 1 byte of LDS per FMA; 64 x 64 (1, 1) has 4x the workgroups for a small C at
+// 2 bytes per FMA; 64 x 32 (SW = 2: 4 x 2 outputs per lane) has 8x.
+template <int TMS_, int TNS_, int BK_, int UNROLL_, int SW_ = 4>
 struct ValuTile {
     static constexpr int TMS = TMS_, TNS = TNS_;
+    static constexpr int SW = SW_;          // columns per lane strip (4 or 2)
     static constexpr int BK = BK_;          // k per LDS stage
     static constexpr int UNROLL = UNROLL_;  // k-loop unroll within a stage
-    static constexpr int BM = 64 * TMS, BN = 64 * TNS;
+    static constexpr int BM = 64 * TMS, BN = 16 * SW * TNS;
     static constexpr int LDA = BM + APAD;  // As row (one k) width
     static constexpr int LDB = BN;         // Bs row width
     static constexpr int A_CH = BM * BK / 4 / NT;  // float4 chunks per lane
@@ -153,7 +156,8 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
                                                    const float *__restrict__ B,
                                                    float beta, float *C,
                                                    int tiles_m, int tiles_n) {
-    constexpr int TM = 4 * Tl::TMS, TN = 4 * Tl::TNS;  // outputs per lane
+    constexpr int TM = 4 * Tl::TMS, TN = Tl::SW * Tl::TNS;  // outputs per lane
+    constexpr int SW = Tl::SW;
     constexpr int BK = Tl::BK;
     __shared__ float As[2][BK * Tl::LDA];
     __shared__ float Bs[2][BK * Tl::LDB];
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
         if (more) load_tile<Tl, VEC>(pf, A, B, M, N, K, cRow, cCol, (kt + 1) * BK, tid);
 
         const float *as = As[cur] + wm + lr * 4;
-        const float *bs = Bs[cur] + wn + lc * 4;
+        const float *bs = Bs[cur] + wn + lc * SW;
         // The 128 x 128 tile unrolls by 2 only: a full unroll lets the
         // scheduler hoist all k-steps' LDS reads and pushes the lane past 256
         // VGPRs. The small tiles (one wave per SIMD at small N) unroll fully,
@@ -203,8 +207,13 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
             }
 #pragma unroll
             for (int s = 0; s < Tl::TNS; ++s) {
-                const float4 b = bmb::ld4(bs + k * Tl::LDB + 32 * s);
-                rb[4 * s + 0] = b.x; rb[4 * s + 1] = b.y; rb[4 * s + 2] = b.z; rb[4 * s + 3] = b.w;
+                if (SW == 4) {
+                    const float4 b = bmb::ld4(bs + k * Tl::LDB + 32 * s);
+                    rb[4 * s + 0] = b.x; rb[4 * s + 1] = b.y; rb[4 * s + 2] = b.z; rb[4 * s + 3] = b.w;
+                } else {
+                    const float2 b = *reinterpret_cast<const float2 *>(bs + k * Tl::LDB + 16 * s);
+                    rb[2 * s + 0] = b.x; rb[2 * s + 1] = b.y;
+                }
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -217,16 +226,16 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
     }
 
     // Epilogue. Row of acc[i][.]: wm + (i/4)*32 + lr*4 + i%4; column of
-    // acc[.][h*4+x]: wn + h*32 + lc*4 + x.
+    // acc[.][h*SW+x]: wn + h*8*SW + lc*SW + x.
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int r = cRow + wm + (i >> 2) * 32 + lr * 4 + (i & 3);
         if (r >= M) continue;
 #pragma unroll
         for (int h = 0; h < Tl::TNS; ++h) {
-            const int c = cCol + wn + h * 32 + lc * 4;
+            const int c = cCol + wn + h * 8 * SW + lc * SW;
             float *dst = C + (size_t)r * N + c;
-            if (VEC && c + 3 < N) {
+            if (VEC && SW == 4 && c + 3 < N) {
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (beta != 0.0f) o = bmb::ld4(dst);
                 o.x = epilogue(acc[i][h * 4 + 0], alpha, beta, &o.x);
@@ -234,10 +243,16 @@ __global__ __launch_bounds__(NT) void sgemm_valu_k(int M, int N, int K,
                 o.z = epilogue(acc[i][h * 4 + 2], alpha, beta, &o.z);
                 o.w = epilogue(acc[i][h * 4 + 3], alpha, beta, &o.w);
                 bmb::st4(dst, o);
+            } else if (VEC && SW == 2 && c + 1 < N) {
+                float2 o = make_float2(0.f, 0.f);
+                if (beta != 0.0f) o = *reinterpret_cast<const float2 *>(dst);
+                o.x = epilogue(acc[i][h * 2 + 0], alpha, beta, &o.x);
+                o.y = epilogue(acc[i][h * 2 + 1], alpha, beta, &o.y);
+                *reinterpret_cast<float2 *>(dst) = o;
             } else {
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    if (c + x < N) dst[x] = epilogue(acc[i][h * 4 + x], alpha, beta, &dst[x]);
+                for (int x = 0; x < SW; ++x)
+                    if (c + x < N) dst[x] = epilogue(acc[i][h * SW + x], alpha, beta, &dst[x]);
             }
         }
     }
@@ -262,6 +277,12 @@ void launch_valu(int M, int N, int K, float alpha, const float *A, const float *
 using TileL = ValuTile<2, 2, 16, 8>;  // 128 x 128: 88
 using TileW = ValuTile<1, 2, 16, 2>;  // 64 x 128: 84.5
 using TileS = ValuTile<1, 1, 32, 8>;  // 64 x 64: 78
+// 64 x 32 with 4 x 2 outputs per lane, for C too small to give every SIMD two
+// waves otherwise (N = 1024: 40.4 TFLOP/s against 37.2 for 64 x 64; N = 512:
+// 12.3 against 8.9). It reads 64 k per stage: one wave per SIMD of 64 x 64
+// tiles, or two of these with 32-deep stages, leave the next stage's HBM
+// latency exposed.
+using TileX = ValuTile<1, 1, 64, 8, 2>;
 
 struct ValuCand {
     int bm, bn;
@@ -286,16 +307,20 @@ int valu_occupancy() {
 // reads less LDS per FMA; a smaller one fills the device at small M x N (at
 // N = 1024: 64 workgroups of 128 x 128 for 256 CUs). Measured on the square
 // sweep: 64 x 64 up to N = 3072 (N = 1024: 37 instead of 11 TFLOP/s),
-// 64 x 128 at the ragged 4097, 128 x 128 from 4096.
+// 64 x 128 at the ragged 4097, 128 x 128 from 4096. Below that, when 64 x 64
+// tiles would put at most one workgroup on each CU (one wave per SIMD, which
+// cannot use the second VALU issue port) and the 64 x 32 tiles fit in one
+// round, the 64 x 32 tile runs two or three waves per SIMD instead.
 int pick_tile(int M, int N) {
     static std::once_flag once[64];
-    static int occ[64][3], cus[64];
+    static int occ[64][4], cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     std::call_once(once[dev], [&] {
         occ[dev][0] = valu_occupancy<TileL>();
         occ[dev][1] = valu_occupancy<TileW>();
         occ[dev][2] = valu_occupancy<TileS>();
+        occ[dev][3] = valu_occupancy<TileX>();
         int c = 0;
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             c <= 0) {
@@ -304,6 +329,9 @@ int pick_tile(int M, int N) {
         }
         cus[dev] = c;
     });
+    const long long tiles_s = (long long)bmb::ceil_div(M, 64) * bmb::ceil_div(N, 64);
+    const long long tiles_x = (long long)bmb::ceil_div(M, 64) * bmb::ceil_div(N, 32);
+    if (tiles_s <= cus[dev] && tiles_x <= (long long)cus[dev] * occ[dev][3]) return 3;
     int best = 0;
     double best_t = -1.0;
     for (int t = 0; t < 3; ++t) {
@@ -326,7 +354,7 @@ int pick_tile(int M, int N) {
     return best;
 }
 
-// tile: 0 = 128x128, 1 = 64x128, 2 = 64x64.
+// tile: 0 = 128x128, 1 = 64x128, 2 = 64x64, 3 = 64x32.
 void run_valu(int tile, int M, int N, int K, float alpha, const float *A, const float *B,
               float beta, float *C) {
     const bool vec = (K % 4 == 0) && (N % 4 == 0) && (((uintptr_t)A & 15) == 0) &&
@@ -334,7 +362,8 @@ void run_valu(int tile, int M, int N, int K, float alpha, const float *A, const 
     switch (tile) {
     case 0: launch_valu<TileL>(M, N, K, alpha, A, B, beta, C, vec); break;
     case 1: launch_valu<TileW>(M, N, K, alpha, A, B, beta, C, vec); break;
-    default: launch_valu<TileS>(M, N, K, alpha, A, B, beta, C, vec); break;
+    case 2: launch_valu<TileS>(M, N, K, alpha, A, B, beta, C, vec); break;
+    default: launch_valu<TileX>(M, N, K, alpha, A, B, beta, C, vec); break;
     }
 }
 
