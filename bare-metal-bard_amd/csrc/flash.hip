@@ -1,11 +1,12 @@
 // Fused causal attention, forward and backward, for gfx950 -- the
 // counterpart of bare-metal-bard's src/flash.cu (API: src/flash.h).
 //
-// The default forward (flash_fwd_h_k, below) carries every fp32 operand as an
-// fp16 hi/lo pair on v_mfma_f32_32x32x16_f16 with exact power-of-two scaling;
-// its comment block gives the error and range argument. The other kernels use
-// chains of v_mfma_f32_32x32x2_f32 (fp32 in, exact fp32 products, fp32
-// accumulate). In that instruction lane l supplies
+// The default forward (flash_fwd_h_k) and backward (flash_dsum_h_k, then
+// flash_bwd_h_k's dK/dV and dQ passes) carry every fp32 operand as an fp16
+// hi/lo pair on v_mfma_f32_32x32x16_f16 with exact power-of-two scaling; the
+// "forward, fp16x3" and "backward, fp16x3" comment blocks give the error and
+// range argument. The other configs' kernels, described first, use chains of
+// v_mfma_f32_32x32x2_f32 (fp32 in, exact fp32 products, fp32 accumulate). In that instruction lane l supplies
 // A[m = l%32][kk = l/32] and B[kk = l/32][n = l%32]; the 32x32 result leaves
 // lane l holding column n = l%32, register r holding row
 // res_row(r, l/32) = 8*(r/4) + 4*(l/32) + r%4. A 32-wide contraction over
