@@ -428,14 +428,23 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // (busy CUs / cus)^0.3; a split adds the partials' round trip and the
 // reduce. Fitted to every tile x {1, 2, 4, 8} splits on the square sweep
 // N = 512 ... 8192 on MI355X, the model picks the measured best plan at every
-// size of that sweep.
+// size of that sweep. With the other split counts below it also picks, for
+// the GPT-2 shapes, the best of a forced sweep over 3 tiles x 11 split counts
+// to within 2%.
 struct B3Cand {
     int bm, bn;
     double tflops;  // fp32-equivalent TFLOP/s when the device is full of them
 };
 constexpr B3Cand CANDS[] = {{256, 256, 417.0}, {128, 128, 326.0}, {64, 64, 233.0}};
 constexpr int N_CANDS = 3;
-constexpr int SPLITS[] = {1, 2, 4, 8};
+// Split counts that are not powers of two fill the device in one round where
+// {2, 4, 8} do not (the GPT-2 weight gradients: 36 tiles of 256 x 256 in 7
+// ranges on 256 CUs, 36 of 128 x 128 in 14 on 512 slots: 18-36% faster). The
+// model undercharges short ranges, so these are only considered when every
+// range keeps MIN_ODD_SPLIT_K of k (a 7-way split of K = 1536, 224 per
+// range, measured 5.5% slower than the 4-way split the model ranked second).
+constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
+constexpr int MIN_ODD_SPLIT_K = 512;
 constexpr double PARTIAL_EXP = 0.5;
 constexpr double FILL_EXP = 0.3;
 constexpr double K_OVERHEAD = 96.0;               // per-item prologue/epilogue, in k
@@ -494,6 +503,7 @@ Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
                 if (splits < 2 || (long long)splits * M * N > max_floats) continue;
+                if ((s & (s - 1)) != 0 && kchunk < MIN_ODD_SPLIT_K) continue;
             }
             const long long items = tiles * splits;
             const long long slots = (long long)cus[dev] * occ[dev][t];
