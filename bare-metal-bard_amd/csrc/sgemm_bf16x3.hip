@@ -429,8 +429,8 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // reduce. Fitted to every tile x {1, 2, 4, 8} splits on the square sweep
 // N = 512 ... 8192 on MI355X, the model picks the measured best plan at every
 // size of that sweep. With the other split counts below it also picks, for
-// the GPT-2 shapes, the best of a forced sweep over 3 tiles x 11 split counts
-// to within 2%.
+// the GPT-2 shapes the best plan of a forced sweep over 3 tiles x 11 split
+// counts, or one within 3% (the sweep's run-to-run spread).
 struct B3Cand {
     int bm, bn;
     double tflops;  // fp32-equivalent TFLOP/s when the device is full of them
