@@ -172,9 +172,10 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     return t;
 }
 
-// Split-K is used only for single problems, and for gemm() only on the null
-// stream: its partials live in leased scratch, whose reuse is ordered by the
-// null stream. max_floats caps the partials (splits * M * N).
+// Split-K is used only for single problems (KERNELS id 9; batched_gemm()
+// never splits) on the null stream: its partials live in leased scratch,
+// whose reuse is ordered by the null stream. max_floats caps the partials
+// (splits * M * N).
 Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
           long long max_floats = MAX_SPLIT_FLOATS) {
     const int cus = device_cus();
@@ -272,16 +273,13 @@ void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// fixed: the split-K partials go to `fixed` (NOALLOC_SPLIT_FLOATS floats, the
-// gemm_noalloc() array) on any stream, instead of leased scratch on the null
-// stream only. Returns false, with nothing launched, only if a plan's
-// partials would not fit there (the planner never picks such a plan).
+// Split-K partials go to leased scratch, used on the null stream only (its
+// reuse is ordered by that stream); on other streams K is not split.
 template <bool TA, bool TB, int EPI = bmb::EPI_BLAS>
-bool dispatch(int batch, int M, int N, int K, float alpha, const float *A,
+void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
               long long sA, const float *B, long long sB, float beta, float *C,
-              long long sC, hipStream_t stream, bmb::EpiArgs ep = {},
-              float *fixed = nullptr) {
-    if (M <= 0 || N <= 0 || batch <= 0) return true;
+              long long sC, hipStream_t stream, bmb::EpiArgs ep = {}) {
+    if (M <= 0 || N <= 0 || batch <= 0) return;
     // 128-bit loads need the contiguous axis of each stored operand to be a
     // multiple of 4 floats, 16-byte aligned bases, and batch strides that keep
     // that alignment.
@@ -289,19 +287,10 @@ bool dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && al16(A) && al16(B) &&
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
     const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
-    Plan p = fixed ? pick(M, N, K, batch, batch == 1, occ, NOALLOC_SPLIT_FLOATS)
-                   : pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
+    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
     float *P = nullptr;
     std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1 && fixed) {
-        if ((long long)p.splits * M * N > NOALLOC_SPLIT_FLOATS) {
-            fprintf(stderr, "gemm_noalloc: %d x %d x %d in %d K ranges needs %lld floats of "
-                    "partials, above the %lld of the fixed scratch array\n", M, N, K, p.splits,
-                    (long long)p.splits * M * N, NOALLOC_SPLIT_FLOATS);
-            return false;
-        }
-        P = fixed;
-    } else if (p.splits > 1) {
+    if (p.splits > 1) {
         lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
@@ -313,7 +302,7 @@ bool dispatch(int batch, int M, int N, int K, float alpha, const float *A,
         case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
         case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
         }
-        return true;
+        return;
     }
     switch (p.tile.kind) {
     case TileKind::L:
@@ -329,17 +318,15 @@ bool dispatch(int batch, int M, int N, int K, float alpha, const float *A,
         launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
         break;
     }
-    return true;
 }
 
-bool gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
+void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
               const float *A, long long sA, const float *B, long long sB,
-              float beta, float *C, long long sC, hipStream_t stream, float *fixed = nullptr) {
-    const bmb::EpiArgs ep{};
-    if (!ta && !tb)     return dispatch<false, false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
-    else if (!ta && tb) return dispatch<false, true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
-    else if (ta && !tb) return dispatch<true,  false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
-    else                return dispatch<true,  true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, ep, fixed);
+              float beta, float *C, long long sC, hipStream_t stream) {
+    if (!ta && !tb)     dispatch<false, false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
+    else if (!ta && tb) dispatch<false, true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
+    else if (ta && !tb) dispatch<true,  false>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
+    else                dispatch<true,  true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
 }
 
 }  // namespace
