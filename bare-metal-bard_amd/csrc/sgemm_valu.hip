@@ -72,6 +72,20 @@ struct ValuTile {
     static constexpr int KCH = BK / 4;             // float4 chunks per A row
 };
 
+// A chunk e (four consecutive k of one row m): four lanes along k (one
+// 64-byte row segment), then consecutive rows, then the next segment. The
+// transposed LDS stores of a wave then cover 16 rows of 4 segments each, so
+// every bank takes one of them (row stride BM + 4: segments 16 banks apart);
+// with 8 or 16 lanes along k they would fall on the same 4 offsets (2- and
+// 4-way conflicts for 32- and 64-deep stages).
+template <class Tl>
+__device__ __forceinline__ void a_chunk(int e, int &m, int &kc) {
+    static_assert(Tl::BK % 16 == 0, "whole 16-k segments per stage");
+    const int kq = e & 3, kseg = e / (4 * Tl::BM);
+    m = (e >> 2) % Tl::BM;
+    kc = (kseg * 4 + kq) * 4;
+}
+
 // Per-thread share of one k-tile of A (BM x BK) and B (BK x BN).
 template <class Tl>
 struct Prefetch {
@@ -83,11 +97,12 @@ template <class Tl, bool VEC>
 __device__ __forceinline__ void load_tile(Prefetch<Tl> &p, const float *A,
                                           const float *B, int M, int N, int K,
                                           int cRow, int cCol, int k0, int tid) {
-    // A chunk e = tid + r*NT: row m = e / KCH, k offset (e % KCH) * 4.
+    // A chunk e = tid + r*NT (a_chunk).
 #pragma unroll
     for (int r = 0; r < Tl::A_CH; ++r) {
         const int e = tid + r * NT;
-        const int m = e / Tl::KCH, kc = (e % Tl::KCH) * 4;
+        int m, kc;
+        a_chunk<Tl>(e, m, kc);
         const int gm = cRow + m, gk = k0 + kc;
         if (VEC) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -136,7 +151,8 @@ __device__ __forceinline__ void store_tile(const Prefetch<Tl> &p, float *As,
 #pragma unroll
     for (int r = 0; r < Tl::A_CH; ++r) {
         const int e = tid + r * NT;
-        const int m = e / Tl::KCH, kc = (e % Tl::KCH) * 4;
+        int m, kc;
+        a_chunk<Tl>(e, m, kc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) As[(kc + i) * Tl::LDA + m] = p.a[r * 4 + i];
     }
@@ -278,8 +294,8 @@ using TileL = ValuTile<2, 2, 16, 8>;  // 128 x 128: 88
 using TileW = ValuTile<1, 2, 16, 2>;  // 64 x 128: 84.5
 using TileS = ValuTile<1, 1, 32, 8>;  // 64 x 64: 78
 // 64 x 32 with 4 x 2 outputs per lane, for C too small to give every SIMD two
-// waves otherwise (N = 1024: 40.4 TFLOP/s against 37.2 for 64 x 64; N = 512:
-// 12.3 against 8.9). It reads 64 k per stage: one wave per SIMD of 64 x 64
+// waves otherwise (N = 1024: 51.0 TFLOP/s against 37.0 for 64 x 64; N = 512:
+// 13.7 against 8.9). It reads 64 k per stage: one wave per SIMD of 64 x 64
 // tiles, or two of these with 32-deep stages, leave the next stage's HBM
 // latency exposed.
 using TileX = ValuTile<1, 1, 64, 8, 2>;
