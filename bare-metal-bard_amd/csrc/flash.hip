@@ -593,14 +593,26 @@ struct FwdSmemH {
     static size_t bytes(int waves) { return SLOTS + 2 * 2 * waves * sizeof(float); }
 };
 
-// Half-index of key kk (0..31) in V^T row d: 16-key groups in the order 0-3,
-// 8-11, 4-7, 12-15, and the four 16-byte chunks of the row XOR-swizzled by
-// d/16, so that the 32-bit stores of the rows d, d+16, d+32, d+48 from one
-// store phase fall in different banks.
-__device__ __forceinline__ int vt_pos(int d, int kk) {
-    const int p = (kk & 16) | (((kk >> 2) & 1) << 3) | (((kk >> 3) & 1) << 2) | (kk & 3);
-    return p ^ (((d >> 4) & 3) << 3);
+// Half-index of key kk (0..31) in a V^T row: 16-key groups in the order 0-3,
+// 8-11, 4-7, 12-15 (the k order of the P fragment taken from the score
+// accumulators).
+__device__ __forceinline__ int vt_pos(int kk) {
+    return (kk & 16) | (((kk >> 2) & 1) << 3) | (((kk >> 3) & 1) << 2) | (kk & 3);
 }
+
+// LDS slot of transposed row d (a head dim) of a V^T, Q^T, dO^T or K^T plane
+// of 80-byte rows: rows permute within each group of four by d bits 4 and 5.
+// gfx950 serves a 128-bit LDS read 16 lanes per cycle, in the lane groups
+// {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (and the same over lanes
+// 32-63), and a 32-bit write 32 consecutive lanes per cycle (measured with
+// SQ_LDS_BANK_CONFLICT). The 80-byte stride alone spreads the 16 rows of a
+// read group over 16 distinct 16-byte slots; the stores of one phase write
+// rows d = 4j + i (j = 0..15 at head size 64) at one or two key words, which
+// the stride alone folds onto four 16-bank blocks, and the permutation
+// spreads over all 64 banks. Reads and stores are then conflict-free at head
+// sizes 32 and 64; at 128 a store phase writes 32 rows at one key word, at
+// least two lanes per bank for any row placement.
+__device__ __forceinline__ int t_row(int d) { return d ^ ((d >> 5) & 1) ^ (((d >> 4) & 1) << 1); }
 
 // A 32-key tile of K and V for the fp16x3 forward in flight from global memory
 // to LDS. Thread tid holds float4 column c = tid % G (G = HS/4 lanes per row) of
@@ -694,7 +706,7 @@ struct KVTileH {
             for (int i = 0; i < 4; ++i) {
                 unsigned hi, lo;
                 split2(a0[i], a1[i], hi, lo);
-                const int vo = ((c + i) * S::LDV + vt_pos(c + i, 2 * p)) * 2;
+                const int vo = (t_row(c + i) * S::LDV + vt_pos(2 * p)) * 2;
                 *reinterpret_cast<unsigned *>(buf + S::OFF_VH + vo) = hi;
                 *reinterpret_cast<unsigned *>(buf + S::OFF_VL + vo) = lo;
             }
@@ -792,11 +804,10 @@ __device__ __forceinline__ void fwd_tile_h(const char *buf, const h8 (&qh)[HS / 
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
         const int row = d * 32 + l32;
-        const char *vr = buf + S::OFF_VH + row * S::LDV * 2;
-        const int sw = ((row >> 4) & 3) << 4;  // chunk swizzle of vt_pos, in bytes
+        const char *vr = buf + S::OFF_VH + t_row(row) * S::LDV * 2;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int off = (32 * ks + 16 * hf) ^ sw;
+            const int off = 32 * ks + 16 * hf;
             const h8 ah = *reinterpret_cast<const h8 *>(vr + off);
             const h8 al = *reinterpret_cast<const h8 *>(vr + (S::OFF_VL - S::OFF_VH) + off);
             o[d] = mfma_h(ah, ph[ks], o[d]);
@@ -1589,10 +1600,6 @@ struct BwdSmemH {
     static constexpr size_t KV_BYTES = 2 * (size_t)KV_BUF, Q_BYTES = 2 * (size_t)Q_BUF;
 };
 
-// Half-index of key kk in a K^T row d of the dQ pass: natural order, 16-byte
-// chunks XOR-swizzled by d/16 as in vt_pos.
-__device__ __forceinline__ int kt_pos(int d, int kk) { return kk ^ (((d >> 4) & 3) << 3); }
-
 // Split a scaled pair and store it in two planes (hi at off, lo at off + dlo).
 __device__ __forceinline__ void put2(char *buf, int off, int dlo, float a, float b) {
     unsigned hi, lo;
@@ -1666,7 +1673,7 @@ struct QOTileH {
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int to = ((c + i) * S::LDT + vt_pos(c + i, 2 * p)) * 2;
+                const int to = (t_row(c + i) * S::LDT + vt_pos(2 * p)) * 2;
                 const unsigned sel = (i & 1) ? 0x07060302u : 0x05040100u;  // high / low halves
                 const unsigned w0 = (i < 2) ? 0 : 1;
                 auto pick = [&](const uint2 (&x)[2]) {
@@ -1772,12 +1779,11 @@ __device__ __forceinline__ void kv_tile_h(const char *buf, const h8 (&kh)[HS / 1
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
         const int row = d * 32 + l32;
-        const int sw = ((row >> 4) & 3) << 4;
-        const char *orow = buf + S::OFF_OTH + row * S::LDT * 2;
-        const char *qrow = buf + S::OFF_QTH + row * S::LDT * 2;
+        const char *orow = buf + S::OFF_OTH + t_row(row) * S::LDT * 2;
+        const char *qrow = buf + S::OFF_QTH + t_row(row) * S::LDT * 2;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int off = (32 * ks + 16 * hf) ^ sw;
+            const int off = 32 * ks + 16 * hf;
             const h8 oh = *reinterpret_cast<const h8 *>(orow + off);
             const h8 ol = *reinterpret_cast<const h8 *>(orow + S::TPLANE + off);
             const h8 qh = *reinterpret_cast<const h8 *>(qrow + off);
@@ -2052,7 +2058,7 @@ __device__ __forceinline__ void bwd_dq_h_block(char *smem, float *__restrict__ d
             const float a1[4] = {kr[ps][1].x, kr[ps][1].y, kr[ps][1].z, kr[ps][1].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                put2(buf, ((c + i) * S::LDT + kt_pos(c + i, 2 * p)) * 2, S::TPLANE,
+                put2(buf, (t_row(c + i) * S::LDT + 2 * p) * 2, S::TPLANE,
                      ldexpf(a0[i], sk), ldexpf(a1[i], sk));
         }
     };
@@ -2108,11 +2114,10 @@ __device__ __forceinline__ void bwd_dq_h_block(char *smem, float *__restrict__ d
 #pragma unroll
                 for (int d = 0; d < DT; ++d) {
                     const int row = d * 32 + l32;
-                    const int sw = ((row >> 4) & 3) << 4;
-                    const char *kt = buf + row * S::LDT * 2;
+                    const char *kt = buf + t_row(row) * S::LDT * 2;
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const int off = (32 * ks + 16 * hf) ^ sw;
+                        const int off = 32 * ks + 16 * hf;
                         const h8 bh8 = *reinterpret_cast<const h8 *>(kt + off);
                         const h8 bl8 = *reinterpret_cast<const h8 *>(kt + S::TPLANE + off);
                         dq[d] = mfma_h(ah[ks], bh8, dq[d]);
