@@ -22,9 +22,16 @@
 //   A, transA = true : As[k][m] (row stride BM + 8)  -> 32-bit fragment reads
 //   B, transB = false: Bs[k][n] (row stride BN + 8)  -> 32-bit fragment reads
 //   B, transB = true : Bs[n][k] (row stride BK + 4)  -> 128-bit fragment reads
-// The +4 pad spreads 16 consecutive rows of a 128-bit read over all 64 banks;
-// the +8 pad puts the two half-waves of a 32-bit read (rows 4 apart) in
-// opposite halves of the banks.
+// gfx950 serves a 128-bit LDS read 16 lanes per cycle, in the lane groups
+// {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (and the same over lanes
+// 32-63), and a 32-bit read 32 consecutive lanes per cycle (measured with
+// SQ_LDS_BANK_CONFLICT). With the +4 pad a k-contiguous row is 9 16-byte
+// slots long, so the 16 rows of a 128-bit read group (distinct residues mod
+// 16) fall in 16 distinct slots. A 32-bit read has each half-wave read 32
+// consecutive floats of one row: distinct banks with any pad (the +8 keeps
+// the two half-waves, rows 4 apart, in opposite bank halves, which the
+// hardware does not need since it serves them in separate cycles). The
+// counter reads no conflict cycle for these layouts.
 //
 // Schedule. K is consumed in tiles of BK (a multiple of 16: an even number of
 // 8-k groups) through two LDS stages. Fragments are double-buffered in
