@@ -1522,7 +1522,9 @@ flash_bwd_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
 // dS's times Q's or K's), rescaled when it grows, so no operand exceeds 2^15.
 
 // Per (head, 32-row tile): D rows as flash_dsum_k, and tmax = (max |Q|,
-// max |dO|, max |K|, max |D|). A workgroup is one tile: 32 rows x HS/4 lanes.
+// max |dO|, 0, max |D|). The dK/dV pass fills in the third component, max |K|,
+// from the key rows it loads anyway, for the dQ pass. A workgroup is one
+// tile: 32 rows x HS/4 lanes.
 template <int HS>
 __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
     float *__restrict__ dsum, float4 *__restrict__ tmax, const float *__restrict__ dout,
@@ -1537,7 +1539,7 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
     const int t = tile * 32 + tid / LPR;
     const int h = bh % NH, b = bh / NH;
     const size_t C = (size_t)NH * HS;
-    float s = 0.0f, mq = 0.0f, mo = 0.0f, mk = 0.0f;
+    float s = 0.0f, mq = 0.0f, mo = 0.0f;
     if (t < T) {
         const size_t off = ((size_t)b * T + t) * C + (size_t)h * HS + sub * 4;
         const float4 a = bmb::ld4(dout + off), c = bmb::ld4(out + off);
@@ -1545,19 +1547,16 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
         mo = absmax4(a);
         const float *qr = qkv + ((size_t)b * T + t) * 3 * C + (size_t)h * HS + sub * 4;
         mq = absmax4(bmb::ld4(qr));
-        mk = absmax4(bmb::ld4(qr + C));
     }
 #pragma unroll
     for (int w = 1; w < LPR; w <<= 1) s += __shfl_xor(s, w);
     if (t < T && sub == 0) dsum[(size_t)bh * T + t] = s;
     mq = wave_max_nonneg(mq);
     mo = wave_max_nonneg(mo);
-    mk = wave_max_nonneg(mk);
     float md = wave_max_nonneg(fabsf(s));
     if ((tid & 63) == 0) {
         red[0][tid >> 6] = mq;
         red[1][tid >> 6] = mo;
-        red[2][tid >> 6] = mk;
         red[3][tid >> 6] = md;
     }
     __syncthreads();
@@ -1566,10 +1565,9 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
         for (int w = 1; w < NW; ++w) {
             mq = fmaxf(mq, red[0][w]);
             mo = fmaxf(mo, red[1][w]);
-            mk = fmaxf(mk, red[2][w]);
             md = fmaxf(md, red[3][w]);
         }
-        tmax[(size_t)bh * ntiles + tile] = make_float4(mq, mo, mk, md);
+        tmax[(size_t)bh * ntiles + tile] = make_float4(mq, mo, 0.0f, md);
     }
     if (t < T && (kv_zero | q_zero) != 0) {
         const int blk = t / blk_rows;
@@ -1823,7 +1821,7 @@ __device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ d
                                                const float *__restrict__ dout,
                                                const float *__restrict__ lse,
                                                const float *__restrict__ dsum,
-                                               const float4 *__restrict__ tmax, int T, int NH,
+                                               float4 *tmax, int T, int NH,
                                                int kblk, int bh, float scale, float qscale,
                                                float *__restrict__ ws, int *__restrict__ ws_exp,
                                                int tq0, int tq1, bool accumulate) {
@@ -1848,7 +1846,7 @@ __device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ d
     int evw;
     {
         float kq[HH], vq[HH];
-        float ak = 0.0f, av = 0.0f;
+        float ak = 0.0f, av = 0.0f, araw = 0.0f;
 #pragma unroll
         for (int j = 0; j < HH; j += 4) {
             float4 kv = zero4(), vv = zero4();
@@ -1861,8 +1859,14 @@ __device__ __forceinline__ void bwd_kv_h_block(char *smem, float *__restrict__ d
             vq[j + 0] = vv.x; vq[j + 1] = vv.y; vq[j + 2] = vv.z; vq[j + 3] = vv.w;
             ak = fmaxf(ak, absmax4(make_float4(kq[j], kq[j + 1], kq[j + 2], kq[j + 3])));
             av = fmaxf(av, absmax4(vv));
+            araw = fmaxf(araw, absmax4(kv));
         }
         evw = max_exp(wave_max_nonneg(av));
+        // max |K| of this wave's key tile (its 32 rows): the dQ pass scales
+        // its K^T tiles by it. Both halves of a split block store the same
+        // value.
+        araw = wave_max_nonneg(araw);
+        if (active && lane == 0) tmax[(size_t)bh * ntiles + k0w / 32].z = araw;
         const int ek = max_exp(pair_max(ak)), ev = max_exp(pair_max(av));
         fk = ek == NOEXP ? 0.0f : ldexpf(1.0f, ek - 14);
         fv = ev == NOEXP ? 0.0f : ldexpf(1.0f, ev - 14);
@@ -2158,7 +2162,7 @@ template <int HS, int WPB, int MODE, int MINW>
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(MINW))) void
 flash_bwd_h_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
               const float *__restrict__ dout, const float *__restrict__ lse,
-              const float *__restrict__ dsum, const float4 *__restrict__ tmax, int T, int NH,
+              const float *__restrict__ dsum, float4 *tmax, int T, int NH,
               float scale, float qscale, float *__restrict__ ws, int *__restrict__ ws_exp,
               const Items items, const int *__restrict__ sched_off,
               const unsigned *__restrict__ sched_ent) {
@@ -2686,10 +2690,10 @@ bool run_bwd_h(float *dqkv, float *dsum, const float *dout, const float *qkv, co
                 q_sc.zero_mask);
     const float scale = 1.0f / sqrtf((float)HS);
     bmb::launch(kkv, dim3(kv_sc.wgs), dim3(threads), S::KV_BYTES, nullptr, dqkv, qkv, dout, lse,
-                dsum, (const float4 *)tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
+                dsum, tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
                 kv_sc.items, (const int *)kv_sc.off, (const unsigned *)kv_sc.ent);
     bmb::launch(kq, dim3(q_sc.wgs), dim3(threads), S::Q_BYTES, nullptr, dqkv, qkv, dout, lse,
-                dsum, (const float4 *)tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
+                dsum, tmax, T, NH, scale, scale * LOG2E, ws, ws_exp,
                 q_sc.items, (const int *)q_sc.off, (const unsigned *)q_sc.ent);
     return true;
 }
