@@ -16,8 +16,9 @@
 // consecutive-k bf16 of row (A) or column (B) l % 32, k = 8 * (l / 32) + 0..7;
 // the D layout matches v_mfma_f32_32x32x2_f32.
 //
-// Tiles. 256x256 (8 waves of 128x64), 128x128 (4 waves of 64x64) and 64x64
-// (4 waves of 32x32) outputs, K in stages of 32 (two 16-k MFMA steps), and a
+// Tiles. 256x256 (8 waves of 128x64), 128x256 (8 waves of 64x64), 128x128
+// (4 waves of 64x64) and 64x64 (4 waves of 32x32) outputs, K in stages of 32
+// (two 16-k MFMA steps), and a
 // split of K into ranges whose fp32 partials one reduce adds in range order
 // (deterministic). A planner picks tile and split per shape, as gemm() does
 // for the fp32 MFMA path: the 256x256 tile alone leaves most CUs idle below
@@ -79,6 +80,7 @@ struct B3Tile {
 using TileL = B3Tile<256, 256, 2, 4>;
 using TileM = B3Tile<128, 128, 2, 2>;
 using TileS = B3Tile<64, 64, 2, 2>;
+using TileT = B3Tile<128, 256, 2, 4>;
 
 // Offset (in bf16) of element k (a multiple of 4) of LDS row `row`. Rows are
 // 64 bytes (four 16-byte chunks); row r is stored in slot p = r ^ ((r >> 2)
@@ -432,22 +434,24 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // ------------------------------------------------------------- host side
 
 // Tile and split choice, the fp32 MFMA planner's time model (mfma_gemm.hip)
-// with this path's own measured constants: a work item is one output tile
-// over one K range; the device runs cus x occupancy of them per round; a
-// part-filled last round runs each CU's items faster by (held / fit)^0.5,
-// and a single round that leaves CUs idle runs faster again by
-// (busy CUs / cus)^0.3; a split adds the partials' round trip and the
-// reduce. Fitted to every tile x {1, 2, 4, 8} splits on the square sweep
-// N = 512 ... 8192 on MI355X, the model picks the measured best plan at every
-// size of that sweep. With the other split counts below it also picks, for
-// the GPT-2 shapes the best plan of a forced sweep over 3 tiles x 11 split
-// counts, or one within 3% (the sweep's run-to-run spread).
+// with this path's own constants: a work item is one output tile over one K
+// range; the device runs cus x occupancy of them per round; a part-filled
+// last round runs each CU's items faster by (held / fit)^PARTIAL_EXP, and a
+// single round that leaves CUs idle runs faster again by
+// (busy CUs / cus)^FILL_EXP; a split adds the partials' round trip and the
+// reduce. The tile rates and PARTIAL_EXP are fitted to a forced sweep on
+// MI355X of every tile x split count below over the GPT-2 shapes and the
+// square sweep N = 512 ... 8192 (810 timed plans): the model's plan is the
+// measured best, or within 3% of it (the sweep's run-to-run spread), on all
+// of them but N = 2048 (5%). The 128 x 256 tile serves the N = 768 and
+// 3072-wide GPT-2 layers with K = 768 or 3072 (4-10% faster than 128 x 128
+// there); a 256 x 128 tile was never chosen and is not built.
 struct B3Cand {
     int bm, bn;
-    double tflops;  // fp32-equivalent TFLOP/s when the device is full of them
+    double tflops;  // fitted fp32-equivalent TFLOP/s when the device is full of them
 };
-constexpr B3Cand CANDS[] = {{256, 256, 417.0}, {128, 128, 326.0}, {64, 64, 233.0}};
-constexpr int N_CANDS = 3;
+constexpr B3Cand CANDS[] = {{256, 256, 452.0}, {128, 128, 326.0}, {64, 64, 233.0}, {128, 256, 345.0}};
+constexpr int N_CANDS = 4;
 // Split counts that are not powers of two fill the device in one round where
 // {2, 4, 8} do not (the GPT-2 weight gradients: 36 tiles of 256 x 256 in 7
 // ranges on 256 CUs, 36 of 128 x 128 in 14 on 512 slots: 18-36% faster). The
@@ -456,7 +460,7 @@ constexpr int N_CANDS = 3;
 // range, measured 5.5% slower than the 4-way split the model ranked second).
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
 constexpr int MIN_ODD_SPLIT_K = 512;
-constexpr double PARTIAL_EXP = 0.5;
+constexpr double PARTIAL_EXP = 0.63;
 constexpr double FILL_EXP = 0.3;
 constexpr double K_OVERHEAD = 96.0;               // per-item prologue/epilogue, in k
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
@@ -492,6 +496,7 @@ Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
         occ[dev][0] = occupancy_of<TileL>();
         occ[dev][1] = occupancy_of<TileM>();
         occ[dev][2] = occupancy_of<TileS>();
+        occ[dev][3] = occupancy_of<TileT>();
         int c = 0;
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             c <= 0) {
@@ -581,7 +586,8 @@ void run_tiles(const Plan &p, int M, int N, int K, float alpha, const float *A, 
     switch (p.tile) {
     case 0: run_plan<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
     case 1: run_plan<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
-    default: run_plan<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
+    case 2: run_plan<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
+    default: run_plan<TileT, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
     }
 }
 
