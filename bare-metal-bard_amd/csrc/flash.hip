@@ -1532,7 +1532,7 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
     float *__restrict__ dqkv, int blk_rows, unsigned long long kv_zero,
     unsigned long long q_zero) {
     constexpr int LPR = HS / 4, NT = 32 * LPR, NW = NT / 64;
-    __shared__ float red[4][NW];
+    __shared__ float red[3][NW];  // per wave: max |Q|, max |dO|, max |D|
     const int ntiles = (T + 31) / 32;
     const int tile = blockIdx.x % ntiles, bh = blockIdx.x / ntiles;
     const int tid = threadIdx.x, sub = tid % LPR;
@@ -1557,7 +1557,7 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
     if ((tid & 63) == 0) {
         red[0][tid >> 6] = mq;
         red[1][tid >> 6] = mo;
-        red[3][tid >> 6] = md;
+        red[2][tid >> 6] = md;
     }
     __syncthreads();
     if (tid == 0) {
@@ -1565,7 +1565,7 @@ __global__ __launch_bounds__(8 * HS) void flash_dsum_h_k(
         for (int w = 1; w < NW; ++w) {
             mq = fmaxf(mq, red[0][w]);
             mo = fmaxf(mo, red[1][w]);
-            md = fmaxf(md, red[3][w]);
+            md = fmaxf(md, red[2][w]);
         }
         tmax[(size_t)bh * ntiles + tile] = make_float4(mq, mo, 0.0f, md);
     }

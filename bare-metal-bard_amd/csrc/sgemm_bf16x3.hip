@@ -444,7 +444,7 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // square sweep N = 512 ... 8192 (810 timed plans): the model's plan is the
 // measured best, or within 3% of it (the sweep's run-to-run spread), on all
 // of them but N = 2048 (5%). The 128 x 256 tile serves the N = 768 and
-// 3072-wide GPT-2 layers with K = 768 or 3072 (4-10% faster than 128 x 128
+// 3072-wide GPT-2 layers with K = 768 or 3072 (4-9% faster than 128 x 128
 // there); a 256 x 128 tile was never chosen and is not built.
 struct B3Cand {
     int bm, bn;
