@@ -96,6 +96,8 @@ _SIGS = {
                             c_vp, c_ll, c_vp, c_ll, c_float, c_vp, c_ll, c_vp]),
     "gemm_noalloc": (c_int, [c_bool, c_bool, c_int, c_int, c_int, c_float, c_vp, c_vp,
                              c_float, c_vp, c_vp]),
+    "gemm_set_math": (c_int, [c_int]),
+    "gemm_get_math": (c_int, []),
     # flash.h
     "flash_attention_forward": (None, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int]),
     "flash_attention_backward": (None, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
@@ -216,6 +218,36 @@ def sgemm(kid: int, M, N, K, alpha, A, B, beta, C) -> None:
 # ------------------------------------------------------------ gemm.h
 def gemm(ta, tb, M, N, K, alpha, A, B, beta, C, stream=0) -> None:
     lib().gemm(bool(ta), bool(tb), M, N, K, alpha, A, B, beta, C, stream or None)
+
+
+GEMM_MATH_BF16X3, GEMM_MATH_FP32 = 0, 1  # include/gemm.h
+
+
+def gemm_set_math(math: int) -> int:
+    """Selects gemm()'s arithmetic for the process; returns the previous mode."""
+    return int(lib().gemm_set_math(int(math)))
+
+
+def gemm_get_math() -> int:
+    return int(lib().gemm_get_math())
+
+
+class gemm_math:
+    """`with bmb.gemm_math(bmb.GEMM_MATH_FP32): ...` runs the block in that
+    mode and restores the previous one."""
+
+    def __init__(self, math):
+        self.math, self.prev = math, None
+
+    def __enter__(self):
+        self.prev = gemm_set_math(self.math)
+        if self.prev < 0:
+            raise ValueError("unknown gemm math mode %r" % (self.math,))
+        return self
+
+    def __exit__(self, *exc):
+        gemm_set_math(self.prev)
+        return False
 
 
 def batched_gemm(ta, tb, batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC,

@@ -29,6 +29,18 @@ inline void allow_smem(K kern, size_t bytes) {
                                            (int)bytes));
 }
 
+// True when `stream` is being captured into a graph. The null stream is never
+// asked (querying it while another stream captures is itself an error).
+inline bool stream_capturing(hipStream_t stream) {
+    if (stream == nullptr) return false;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;  // unknown: behave as under capture (allocate nothing)
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kern)(KArgs...), dim3 grid, dim3 block, size_t smem,
                    hipStream_t stream, Args... args) {

@@ -11,6 +11,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <optional>
 
@@ -172,9 +173,8 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     return t;
 }
 
-// Split-K is used only for single problems (KERNELS id 9; batched_gemm()
-// never splits) on the null stream: its partials live in leased scratch,
-// whose reuse is ordered by the null stream. max_floats caps the partials
+// Split-K is used only for single problems (KERNELS id 9, gemm() in fp32
+// mode; batched_gemm() never splits). max_floats caps the partials
 // (splits * M * N).
 Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
           long long max_floats = MAX_SPLIT_FLOATS) {
@@ -273,12 +273,14 @@ void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Split-K partials go to leased scratch, used on the null stream only (its
-// reuse is ordered by that stream); on other streams K is not split.
+// Split-K partials go to `fixed` (at most fixed_floats), or else to scratch
+// leased for `stream` (reuse ordered by the lease's event); under graph
+// capture, where a lease could allocate, K is not split.
 template <bool TA, bool TB, int EPI = bmb::EPI_BLAS>
 void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
               long long sA, const float *B, long long sB, float beta, float *C,
-              long long sC, hipStream_t stream, bmb::EpiArgs ep = {}) {
+              long long sC, hipStream_t stream, bmb::EpiArgs ep = {},
+              float *fixed = nullptr, long long fixed_floats = 0) {
     if (M <= 0 || N <= 0 || batch <= 0) return;
     // 128-bit loads need the contiguous axis of each stored operand to be a
     // multiple of 4 floats, 16-byte aligned bases, and batch strides that keep
@@ -287,11 +289,12 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && al16(A) && al16(B) &&
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
     const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
-    Plan p = pick(M, N, K, batch, batch == 1 && stream == nullptr, occ);
-    float *P = nullptr;
+    const bool may_split = batch == 1 && (fixed != nullptr || !bmb::stream_capturing(stream));
+    Plan p = pick(M, N, K, batch, may_split, occ, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
+    float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1) {
-        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
+    if (p.splits > 1 && fixed == nullptr) {
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
     }
@@ -329,10 +332,43 @@ void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
     else                dispatch<true,  true >(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream);
 }
 
+// The arithmetic of gemm(), gemm_noalloc() and the GPT's linear layers
+// (gemm_set_math): process-wide, read once per call.
+std::atomic<int> g_math{GEMM_MATH_BF16X3};
+
+bool fp32_math() { return g_math.load(std::memory_order_relaxed) == GEMM_MATH_FP32; }
+
+// gemm() / gemm_noalloc() in fp32 mode: the KERNELS id 9 kernels (fp32
+// matrix-core products), any transposes, split-K into `fixed` or leased
+// scratch.
+void fp32_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
+               const float *B, float beta, float *C, hipStream_t stream, float *fixed,
+               long long fixed_floats) {
+    const bmb::EpiArgs ep{};
+    if (!ta && !tb)
+        dispatch<false, false>(1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, ep, fixed, fixed_floats);
+    else if (!ta && tb)
+        dispatch<false, true>(1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, ep, fixed, fixed_floats);
+    else if (ta && !tb)
+        dispatch<true, false>(1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, ep, fixed, fixed_floats);
+    else
+        dispatch<true, true>(1, M, N, K, alpha, A, 0, B, 0, beta, C, 0, stream, ep, fixed, fixed_floats);
+}
+
 }  // namespace
 
 void bmb::gemm_bias_nt(int M, int N, int K, const float *A, const float *W, const float *bias,
                        float *C, float *gelu_out) {
+    if (fp32_math()) {
+        const bmb::EpiArgs ep{bias, gelu_out, nullptr};
+        if (gelu_out != nullptr)
+            dispatch<false, true, bmb::EPI_BIAS_GELU>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0,
+                                                      nullptr, ep);
+        else
+            dispatch<false, true, bmb::EPI_BIAS>(1, M, N, K, 1.0f, A, 0, W, 0, 0.0f, C, 0,
+                                                 nullptr, ep);
+        return;
+    }
     bmb::bf16x3_gemm(false, true, M, N, K, 1.0f, A, W, 0.0f, C, nullptr,
                      gelu_out != nullptr ? bmb::EPI_BIAS_GELU : bmb::EPI_BIAS, bias, gelu_out,
                      nullptr, nullptr, 0);
@@ -340,6 +376,11 @@ void bmb::gemm_bias_nt(int M, int N, int K, const float *A, const float *W, cons
 
 void bmb::gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B,
                             const float *pre, float *C) {
+    if (fp32_math()) {
+        dispatch<false, false, bmb::EPI_GELU_GRAD>(1, M, N, K, 1.0f, A, 0, B, 0, 0.0f, C, 0,
+                                                   nullptr, bmb::EpiArgs{nullptr, nullptr, pre});
+        return;
+    }
     bmb::bf16x3_gemm(false, false, M, N, K, 1.0f, A, B, 0.0f, C, nullptr, bmb::EPI_GELU_GRAD,
                      nullptr, nullptr, pre, nullptr, 0);
 }
@@ -380,6 +421,10 @@ extern "C" {
 void gemm(bool transA, bool transB, int M, int N, int K, float alpha,
           const float *A, const float *B, float beta, float *C,
           hipStream_t stream) {
+    if (fp32_math()) {
+        fp32_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream, nullptr, 0);
+        return;
+    }
     bmb::bf16x3_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream, bmb::EPI_BLAS,
                      nullptr, nullptr, nullptr, nullptr, 0);
 }
@@ -402,11 +447,25 @@ int gemm_noalloc(bool transA, bool transB, int M, int N, int K, float alpha, con
     if (M <= 0 || N <= 0) return 0;
     float *fixed = noalloc_scratch();
     if (fixed == nullptr) return -1;
-    return bmb::bf16x3_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream,
-                            bmb::EPI_BLAS, nullptr, nullptr, nullptr, fixed,
-                            NOALLOC_SPLIT_FLOATS)
-               ? 0
-               : -1;
+    if (fp32_math()) {
+        fp32_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream, fixed,
+                  NOALLOC_SPLIT_FLOATS);
+        return 0;
+    }
+    bmb::bf16x3_gemm(transA, transB, M, N, K, alpha, A, B, beta, C, stream, bmb::EPI_BLAS,
+                     nullptr, nullptr, nullptr, fixed, NOALLOC_SPLIT_FLOATS);
+    return 0;
 }
+
+int gemm_set_math(int math) {
+    if (math != GEMM_MATH_BF16X3 && math != GEMM_MATH_FP32) {
+        fprintf(stderr, "gemm_set_math: unknown mode %d (GEMM_MATH_BF16X3 = %d, "
+                        "GEMM_MATH_FP32 = %d)\n", math, GEMM_MATH_BF16X3, GEMM_MATH_FP32);
+        return -1;
+    }
+    return g_math.exchange(math);
+}
+
+int gemm_get_math(void) { return g_math.load(); }
 
 }  // extern "C"

@@ -118,11 +118,22 @@ __device__ __forceinline__ int lds_off(int row, int k) {
     return p * LDK + 8 * ((k >> 3) ^ ((row >> 3) & 3)) + (k & 7);
 }
 
-// x -> (bf16(x), bf16(x - bf16(x))) for four values.
+// The largest float that rounds to a finite bfloat16 (0x7F7F7FFF): above it
+// round-to-nearest gives infinity, although x is finite.
+constexpr float BF16_FINITE_MAX = 0x1.fefffep+127f;
+
+// x -> (hi, lo) = (bf16(c), bf16(x - hi)) for four values, with c = x clamped
+// to +-BF16_FINITE_MAX (one v_med3_f32). For |x| <= BF16_FINITE_MAX, c = x.
+// Above it (finite x up to FLT_MAX, or +-inf) hi is bf16's largest finite
+// value with x's sign and x - hi is exact (Sterbenz) or +-inf, so a huge
+// finite x still splits exactly instead of into (inf, -inf), and an infinite
+// x gives (+-3.39e38, +-inf), whose products with a nonzero b are +-inf and
+// with b = 0 NaN, as in fp32. NaN stays NaN in lo.
 __device__ __forceinline__ void split4(const float (&x)[4], bf16x4 &hi, bf16x4 &lo) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const __bf16 h = (__bf16)x[i];
+        const __bf16 h =
+            (__bf16)__builtin_amdgcn_fmed3f(x[i], -BF16_FINITE_MAX, BF16_FINITE_MAX);
         hi[i] = h;
         lo[i] = (__bf16)(x[i] - (float)h);
     }
@@ -725,8 +736,9 @@ void run_tiles(const Plan &p, int M, int N, int K, float alpha, const float *A, 
 
 // The bf16x3 GEMM behind gemm(), gemm_noalloc() and the GPT's fused linear
 // layers (gemm_fused.hpp). Split-K partials go to `fixed` (at most
-// fixed_floats) on any stream, or else to leased scratch, used only on the null
-// stream (its reuse is ordered by the null stream). The epilogue is one of
+// fixed_floats), or else to scratch leased for `stream` (its reuse is ordered
+// by the lease's event), except under graph capture, where a lease could
+// allocate: there K is not split. The epilogue is one of
 // EPI_BLAS (any transposes), EPI_BIAS / EPI_BIAS_GELU (A @ W^T) and
 // EPI_GELU_GRAD (A @ B). Returns false, with nothing launched, for another
 // combination.
@@ -739,12 +751,12 @@ bool bmb::bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const 
     const int a_contig = ta ? M : K, b_contig = tb ? K : N;
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && (((uintptr_t)A & 15) == 0) &&
                      (((uintptr_t)B & 15) == 0);
-    const bool may_split = fixed != nullptr || stream == nullptr;
+    const bool may_split = fixed != nullptr || !bmb::stream_capturing(stream);
     Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
     if (p.splits > 1 && fixed == nullptr) {
-        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float));
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, false, 0);  // no scratch: no split
     }

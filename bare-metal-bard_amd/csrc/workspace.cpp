@@ -1,8 +1,6 @@
 // Per-device pools of leased scratch buffers (see workspace.hpp).
 #include "workspace.hpp"
 
-#include <hip/hip_runtime_api.h>
-
 #include <mutex>
 #include <vector>
 
@@ -11,6 +9,10 @@ namespace bmb {
 struct ScratchBuffer {
     void *ptr = nullptr;
     size_t cap = 0;
+    // Recorded on the last lessee's stream when it returned the buffer;
+    // `recorded` is false until the first return.
+    hipEvent_t done = nullptr;
+    bool recorded = false;
 };
 
 namespace {
@@ -28,7 +30,8 @@ Pool &pool(int dev, ScratchSlot slot) {
 }
 }  // namespace
 
-ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes) : slot_(slot) {
+ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes, hipStream_t stream)
+    : slot_(slot), stream_(stream) {
     int dev = 0;
     if (slot < 0 || slot >= SCRATCH_SLOTS) return;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
@@ -56,12 +59,18 @@ ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes) : slot_(slot) {
         }
     }
     dev_ = dev;
+    if (buf_->done == nullptr &&
+        hipEventCreateWithFlags(&buf_->done, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        buf_->done = nullptr;
+        return;  // no way to order reuse: no buffer (the destructor puts it back)
+    }
     if (buf_->cap < bytes) {
         if (buf_->ptr != nullptr) {
             // Work queued by an earlier lessee may still read the old buffer.
-            if (hipDeviceSynchronize() != hipSuccess) {
+            if (buf_->recorded && hipEventSynchronize(buf_->done) != hipSuccess) {
                 (void)hipGetLastError();
-                return;  // the destructor puts the buffer back unchanged
+                return;
             }
             (void)hipFree(buf_->ptr);
             buf_->ptr = nullptr;
@@ -74,12 +83,26 @@ ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes) : slot_(slot) {
         }
         buf_->ptr = q;
         buf_->cap = bytes;
+    } else if (buf_->recorded && hipStreamWaitEvent(stream_, buf_->done, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
     }
     ptr_ = buf_->ptr;
 }
 
 ScratchLease::~ScratchLease() {
     if (buf_ == nullptr) return;
+    if (ptr_ != nullptr) {
+        // After everything this lease's caller queued on its stream.
+        if (hipEventRecord(buf_->done, stream_) == hipSuccess) {
+            buf_->recorded = true;
+        } else {
+            (void)hipGetLastError();
+            // Unordered reuse is not allowed: wait for the stream instead.
+            if (hipStreamSynchronize(stream_) != hipSuccess) (void)hipGetLastError();
+            buf_->recorded = false;
+        }
+    }
     Pool &p = pool(dev_, slot_);
     std::lock_guard<std::mutex> lock(p.mu);
     p.idle.push_back(buf_);

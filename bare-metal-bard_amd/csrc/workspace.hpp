@@ -5,24 +5,28 @@
 // tiles of the flash backward). They lease it for the duration of one call
 // from a pool kept per (device, slot):
 //
-//   bmb::ScratchLease ws(bmb::SCRATCH_NN, bytes);
+//   bmb::ScratchLease ws(bmb::SCRATCH_NN, bytes, stream);
 //   if (!ws) ...;            // could not be allocated (the error is cleared)
-//   launch(..., ws.get());   // kernels queued on the null stream
+//   launch(..., ws.get());   // kernels queued on `stream`
 //   // ~ScratchLease returns the buffer to the pool
 //
 // A buffer is held by one lease at a time, so calls made concurrently from
 // several host threads never share one; the pool holds as many buffers as
 // were ever leased at once (per device and slot), whatever the number of
-// threads that come and go. Every user queues its kernels on the null stream
-// of the device, where launches run in submission order whichever host thread
-// made them: the next lessee's kernels therefore run after the previous
-// lessee's, although the buffer returns to the pool as soon as the previous
-// call has queued its work. A buffer that must grow is freed only after the
-// device has gone idle (earlier work may still read it). Buffers are kept
-// until the process ends.
+// threads that come and go. The buffer returns to the pool as soon as the
+// call has queued its work, so reuse is ordered on the device by an event:
+// the lease's destructor records the buffer's event on the lessee's stream
+// (after every kernel the call queued there), and the next lease makes its
+// own stream wait for that event before anything it queues. Two calls on
+// different streams, or on the null stream from several host threads,
+// therefore never touch one buffer at the same time. A buffer that must grow
+// is freed only after its event has completed. Buffers are kept until the
+// process ends.
 #pragma once
 
 #include <stddef.h>
+
+#include <hip/hip_runtime_api.h>
 
 namespace bmb {
 
@@ -36,10 +40,11 @@ enum ScratchSlot {
 struct ScratchBuffer;
 
 // Checks out a buffer of at least `bytes` bytes (256 if 0) of the current
-// device for `slot`; get() is nullptr when it cannot be had.
+// device for `slot`, for kernels queued on `stream` (0: the null stream);
+// get() is nullptr when it cannot be had.
 class ScratchLease {
    public:
-    ScratchLease(ScratchSlot slot, size_t bytes);
+    ScratchLease(ScratchSlot slot, size_t bytes, hipStream_t stream = nullptr);
     ~ScratchLease();
     ScratchLease(const ScratchLease &) = delete;
     ScratchLease &operator=(const ScratchLease &) = delete;
@@ -50,6 +55,7 @@ class ScratchLease {
    private:
     int dev_ = -1;
     ScratchSlot slot_;
+    hipStream_t stream_;
     ScratchBuffer *buf_ = nullptr;
     void *ptr_ = nullptr;
 };

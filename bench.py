@@ -30,7 +30,16 @@ The same JSON line also carries (none of them is `value`):
     on synthetic uniform tokens: tokens/s over the timed steps and the loss
     trajectory;
   * cpu_baseline: the oracle's order-preserving SGEMM and unfused attention
-    on the host's cores (a bounded sample, reported, not a target).
+    on the host's cores (a bounded sample, reported, not a target);
+  * verification: before each timed region, outside it, the result of one
+    launch on the same inputs is checked against the CPU oracle, as the
+    reference's bench does before timing a kernel (src/bench.cu:259-273):
+    sampled rows of every SGEMM (bit-exact for the fp32 VALU ids, within the
+    fp32 summation bound for id 9, within the bf16x3 bound for id 10), batch
+    0 of the attention (out, lse, dq, dk, dv against fp64), sampled rows of
+    every config 3 GEMM in both arithmetic modes, and the GPT step's losses.
+    The errors go into the line (`verification`); if any exceeds its bound
+    the line is still printed and the bench exits with status 1.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--only sgemm|flash] [--flash-sweep] [--quick]
@@ -85,6 +94,16 @@ def parse():
                          "known-size reference dispatch for rocprofv3 --pmc FETCH_SIZE / "
                          "WRITE_SIZE calibration")
     return ap.parse_args()
+
+
+T_START = time.perf_counter()
+
+
+def progress(msg):
+    """One line on stderr per finished part of the run (the JSON line alone
+    goes to stdout)."""
+    print("bench.py [%6.1f s] %s" % (time.perf_counter() - T_START, msg), file=sys.stderr,
+          flush=True)
 
 
 def timed(fn, steps, warmup):
@@ -374,6 +393,71 @@ def sgemm_fn(bmb, kid):
     return bmb.find_kernel(kid)["fn"]
 
 
+U32 = 2.0 ** -24
+
+
+def fp32_order_bound(K):
+    """Normwise bound (max |err| / max |ref|) for an fp32 result whose
+    products are exact and whose only difference from the exact sum is fp32
+    summation: a random-walk model, 4 sqrt(K) 2^-24, plus the epilogue."""
+    import math
+    return 4.0 * math.sqrt(max(K, 1)) * U32 + 4.0 * U32
+
+
+class Verifier:
+    """Results checked against the CPU oracle outside the timed regions;
+    `record` keeps each check's error, bound and verdict for the line."""
+
+    def __init__(self, O):
+        self.O, self.checks, self.failed = O, {}, []
+
+    def record(self, name, err, bound, kind, ok=None, **extra):
+        ok = bool(err <= bound) if ok is None else bool(ok and err <= bound)
+        self.checks[name] = dict({"err": float("%.3g" % err), "bound": float("%.3g" % bound),
+                                  "kind": kind, "ok": ok}, **extra)
+        if not ok:
+            self.failed.append(name)
+        return ok
+
+    def gemm_rows(self, name, got_rows, A_rows, B, tb, N, K, alpha, beta, C0_rows, math_kind,
+                  tol):
+        """got_rows = rows of C = alpha op(A) op(B) + beta C0; A_rows are the
+        matching rows of op(A) (M' x K), B is stored K x N or N x K (tb).
+        math_kind: "seq" (bit-exact against the sequential-fmaf oracle; tb
+        false only), "fp32" or "bf16x3". Every kind is also within `tol`
+        (normwise against fp64)."""
+        import numpy as np
+        O = self.O
+        M = A_rows.shape[0]
+        got_rows = np.asarray(got_rows).reshape(M, N)
+        ref = O.gemm_f64(False, tb, M, N, K, alpha, A_rows, B, beta, C0_rows)
+        err, bad = O.normwise(got_rows, ref)
+        if bad:
+            return self.record(name, float("inf"), tol, math_kind + ": non-finite entries")
+        if math_kind == "seq":
+            want = O.gemm_f32seq(0, 0, M, N, K, alpha, A_rows, B, beta, C0_rows, threads=0)
+            same = bool(np.array_equal(got_rows, want))
+            return self.record(name, err, tol, "bit-exact vs sequential fmaf, normwise vs fp64",
+                               ok=same, bit_exact=same)
+        if math_kind == "fp32":
+            return self.record(name, err, min(tol, fp32_order_bound(K)),
+                               "normwise vs fp64 within the fp32 summation bound")
+        Bop = np.ascontiguousarray(B.reshape(N, K).T if tb else B.reshape(K, N))
+        want = O.gemm_bf16x3_f64(M, N, K, alpha, A_rows, Bop, beta, C0_rows)
+        e3, bad3 = O.normwise(got_rows, want)
+        return self.record(name, e3 if not bad3 else float("inf"), fp32_order_bound(3 * K),
+                           "normwise around the bf16x3 split's exact value (fp32 summation "
+                           "bound of 3K terms); vs fp64 within tol", ok=err <= tol,
+                           vs_fp64=float("%.3g" % err), tol=tol)
+
+
+def sample_rows(n, seed=7, extra=8):
+    import numpy as np
+    r = np.r_[0, 1, 127, 128, n // 2, n - 2, n - 1,
+              np.random.default_rng(seed).integers(0, n, extra)]
+    return np.unique(r[(r >= 0) & (r < n)])
+
+
 def gf(flops, ms):
     return round(flops / ms / 1e6, 1)
 
@@ -416,23 +500,44 @@ def main():
                     "src/bench.cu:226-228; attention q,k,v,dO N(0,1) by Box-Muller)"}
 
     N = args.n
+    V = Verifier(O)
     A = O.fill_xorshift(N * N, 0x12345678).reshape(N, N)
     Bm = O.fill_xorshift(N * N, 0x9ABCDEF0).reshape(N, N)
     C0 = O.fill_xorshift(N * N, 0x0F0F0F0F).reshape(N, N)
     if args.only in (None, "sgemm"):
+        # The problem of size n reads the first n*n floats of each buffer as an
+        # n x n row-major matrix; an xorshift stream's first n*n values are the
+        # n*n stream, so every size sees the bench's seeded matrices.
         smax = max(max(SWEEP_N), N) if extras else N
-        dA = torch.from_numpy(O.fill_xorshift(smax * smax, 0x12345678)).cuda()
-        dB = torch.from_numpy(O.fill_xorshift(smax * smax, 0x9ABCDEF0)).cuda()
-        dC = torch.from_numpy(O.fill_xorshift(smax * smax, 0x0F0F0F0F)).cuda()
-        dA[:N * N].copy_(torch.from_numpy(A.reshape(-1)))
-        dB[:N * N].copy_(torch.from_numpy(Bm.reshape(-1)))
-        dC[:N * N].copy_(torch.from_numpy(C0.reshape(-1)))
+        hA = O.fill_xorshift(smax * smax, 0x12345678)
+        hB = O.fill_xorshift(smax * smax, 0x9ABCDEF0)
+        hC = O.fill_xorshift(smax * smax, 0x0F0F0F0F)
+        dA, dB, dC = (torch.from_numpy(h).cuda() for h in (hA, hB, hC))
+        dV = torch.empty_like(dC)  # the verification launches' output
 
         def sq(kid, n, alpha=1.0, beta=0.5):
             fn = sgemm_fn(bmb, kid)
             return lambda: fn(n, n, n, alpha, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
 
+        def verify_sq(kid, n, alpha=1.0, beta=0.5, extra=8):
+            """One launch into a fresh copy of C, sampled rows against the
+            oracle (outside every timed region)."""
+            dV[:n * n].copy_(torch.from_numpy(hC[:n * n]))
+            sgemm_fn(bmb, kid)(n, n, n, alpha, dA.data_ptr(), dB.data_ptr(), beta, dV.data_ptr())
+            torch.cuda.synchronize()
+            bmb.check("sgemm id %d verification" % kid)
+            rows = sample_rows(n, extra=extra)
+            got = dV[:n * n].view(n, n)[torch.from_numpy(rows).cuda()].cpu().numpy()
+            kind = "seq" if kid <= 8 else ("fp32" if kid == 9 else "bf16x3")
+            progress("verified KERNELS id %d at N=%d" % (kid, n))
+            return V.gemm_rows("sgemm id%d N=%d alpha=%g beta=%g" % (kid, n, alpha, beta), got,
+                               hA[:n * n].reshape(n, n)[rows], hB[:n * n].reshape(n, n), False,
+                               n, n, alpha, beta,
+                               hC[:n * n].reshape(n, n)[rows] if beta != 0 else None, kind,
+                               bmb.find_kernel(kid)["tol"])
+
         flops = 2.0 * N ** 3
+        verify_sq(args.kernel, N)
         ms, wall = timed_steps(sq(args.kernel, N), args.steps, args.warmup, "sgemm")
         st = stats(timed(sq(args.kernel, N), args.steps, 2))  # per-launch spread
         bmb.check("sgemm")
@@ -441,7 +546,7 @@ def main():
         bytes_alg = 4.0 * (3 * N * N + N * N)  # A, B, C read (beta != 0), C written
         line.update({
             "value": round(g, 1), "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
-            "pct_of_peak": round(100 * g / 1e3 / PEAK_FP32_TFLOPS, 1),
+            "pct_of_peak": round(100 * g / 1e3 / own_peak(args.kernel)[0], 1),
             "config": {"workload": "sgemm M=N=K=%d fp32 row-major alpha=1 beta=0.5, "
                                    "KERNELS id %d (%s)" % (N, args.kernel, ent["name"]),
                        "tol": ent["tol"], "algorithmic_gflop": round(flops / 1e9, 2),
@@ -459,10 +564,12 @@ def main():
             "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
         })
 
+        progress("headline SGEMM timed: %.4f ms/step" % ms)
         if extras:
             # Config 1: N=1024, alpha=1, beta=0.
             c1 = {}
             for kid in (8, 9, 10):
+                verify_sq(kid, 1024, 1.0, 0.0)
                 ms1 = timed_burst(sq(kid, 1024, 1.0, 0.0), 20, 5)
                 c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3, ms1)
             line["config1_n1024_gflops"] = c1
@@ -475,14 +582,18 @@ def main():
             for kid in (8, 9, 10):
                 row = {}
                 for n in SWEEP_N:
+                    verify_sq(kid, n, extra=2)
                     reps = 10 if n <= 4096 else 5
                     row[str(n)] = gf(2.0 * n ** 3, timed_burst(sq(kid, n), reps))
                 sweep["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = row
+                progress("config 2 sweep of id %d timed" % kid)
             bmb.check("sgemm sweep")
             line["config2_sweep_gflops"] = sweep
             # The ladder at N=4096.
             ladder = {}
             for kid in range(1, 11):
+                if kid not in (8, 9, 10):  # (verified in the sweep at this size)
+                    verify_sq(kid, N, extra=2)
                 reps, warm = (2, 1) if kid <= 2 else (5, 2)
                 s3 = stats(timed(sq(kid, N), reps, warm))
                 pk, pk_name = own_peak(kid)
@@ -492,18 +603,23 @@ def main():
                     "peak_tflops": round(pk, 1)}
             bmb.check("ladder")
             line["ladder_n%d" % N] = ladder
-            del dA, dB, dC
+            del dA, dB, dC, dV
             torch.cuda.empty_cache()
-            line["config3_gpt_gemm_gflops"] = gpt_shapes(bmb, O, torch)
+            line["config3_gpt_gemm_gflops"] = gpt_shapes(bmb, O, torch, V)
 
     if args.only == "sizes":
         line["sgemm_sizes_gflops"] = sizes_bench(bmb, O, torch)
     if args.only in (None, "flash"):
-        line["flash"] = flash_bench(args, bmb, O, torch, traffic)
+        line["flash"] = flash_bench(args, bmb, O, torch, traffic, V)
     if args.only == "gpt" or (args.only is None and not args.quick):
-        line["config5_gpt_train_step"] = gpt_step_bench(args, bmb, torch)
+        line["config5_gpt_train_step"] = gpt_step_bench(args, bmb, torch, V)
+        if not args.quick:
+            with bmb.gemm_math(bmb.GEMM_MATH_FP32):
+                line["config5_gpt_train_step_fp32_gemm"] = gpt_step_bench(
+                    args, bmb, torch, V, steps=5, warm=2, tag="fp32 GEMM")
 
     if not args.no_cpu and not args.quick:
+        progress("CPU baseline")
         cpu = {}
         if args.only in (None, "sgemm"):
             cpu = cpu_sgemm_baseline(O, A, Bm, C0, N)
@@ -517,7 +633,11 @@ def main():
             if not cpu:
                 cpu = fl
         line["cpu_baseline"] = cpu
+    line["verification"] = {"all_ok": not V.failed, "failed": V.failed, "checks": V.checks}
     print(json.dumps(line))
+    if V.failed:
+        print("bench.py: verification failed: %s" % ", ".join(V.failed), file=sys.stderr)
+        sys.exit(1)
 
 
 def sizes_bench(bmb, O, torch):
@@ -553,45 +673,81 @@ def vendor_sq(torch, dA, dB, dC, N):
     return gf(2.0 * N ** 3, timed_burst(fn, 20))
 
 
-def gpt_shapes(bmb, O, torch):
-    """gemm() at the GPT-2-small training shapes (src/gpt.cu:256-376): the
-    forward is NT (weights stored out x in), the backward dX is NN with
-    beta 0 and dW is TN with beta 1 (accumulate)."""
-    BT, C, V = GPT["BT"], GPT["C"], GPT["V"]
+def gpt_shapes(bmb, O, torch, V):
+    """gemm() at the GPT-2-small training shapes
+    (src/gpt.cu:256-376), in both of gemm()'s arithmetic modes, each against
+    its own ceiling: bf16x3 (the default; 833 TFLOP/s of fp32-equivalent
+    work on three bf16 MFMAs per product) and fp32 (gemm_set_math
+    GEMM_MATH_FP32: fp32 MFMA products, the reference's arithmetic; 157.3).
+    The forward is NT (weights stored out x in), the backward dX is NN with
+    beta 0 and dW is TN with beta 1 (accumulate). Activations N(0, 1),
+    weights N(0, 0.02^2). Before timing, each GEMM's result is checked on
+    sampled rows against the oracle in each mode."""
+    import numpy as np
+    BT, C, Vv = GPT["BT"], GPT["C"], GPT["V"]
     torch.backends.cuda.matmul.allow_tf32 = False  # the vendor comparison stays fp32
     layers = {"qkv": (C, 3 * C), "attn_proj": (C, C), "mlp_fc": (C, 4 * C),
-              "mlp_proj": (4 * C, C), "lm_head": (C, V)}
-    res = {}
+              "mlp_proj": (4 * C, C), "lm_head": (C, Vv)}
+    modes = (("bf16x3", bmb.GEMM_MATH_BF16X3, BF16X3_CEILING_TFLOPS),
+             ("fp32", bmb.GEMM_MATH_FP32, PEAK_FP32_TFLOPS))
+    res = {"units": "GFLOP/s", "ceilings_tflops": {m[0]: round(m[2], 1) for m in modes},
+           "vendor_fp32": "the vendor's fp32 GEMM (hipBLASLt through torch, TF32 off) on the "
+                          "same operands: context, not this build's result"}
+    f32 = dict(device="cuda", dtype=torch.float32)
     for name, (cin, cout) in layers.items():
-        x = torch.from_numpy(O.fill_normal(BT * max(cin, cout), 11)).cuda()
-        w = torch.from_numpy(O.fill_normal(cout * cin, 12, 0.02)).cuda()
-        y = torch.empty(BT * max(cin, cout), device="cuda", dtype=torch.float32)
+        hX = O.fill_normal(BT * cin, 11)
+        hW = O.fill_normal(cout * cin, 12, 0.02)
+        hDY = O.fill_normal(BT * cout, 13)
+        hDW0 = O.fill_normal(cout * cin, 14, 0.02)
+        X, W, DY = (torch.from_numpy(h).to(**f32) for h in (hX, hW, hDY))
+        Y, DX, DW = torch.empty(BT * cout, **f32), torch.empty(BT * cin, **f32), \
+            torch.from_numpy(hDW0).to(**f32)
         fl = 2.0 * BT * cin * cout
-        # forward y[BT,cout] = x[BT,cin] @ w[cout,cin]^T
-        fwd = lambda: bmb.gemm(False, True, BT, cout, cin, 1.0, x.data_ptr(), w.data_ptr(),
-                               0.0, y.data_ptr())
+        # forward Y[BT,cout] = X[BT,cin] @ W[cout,cin]^T
+        fwd = lambda: bmb.gemm(False, True, BT, cout, cin, 1.0, X.data_ptr(), W.data_ptr(),
+                               0.0, Y.data_ptr())
         # dX[BT,cin] = dY[BT,cout] @ W[cout,cin]
-        dxf = lambda: bmb.gemm(False, False, BT, cin, cout, 1.0, y.data_ptr(), w.data_ptr(),
-                               0.0, x.data_ptr())
+        dxf = lambda: bmb.gemm(False, False, BT, cin, cout, 1.0, DY.data_ptr(), W.data_ptr(),
+                               0.0, DX.data_ptr())
         # dW[cout,cin] += dY^T[cout,BT] @ X[BT,cin]
-        dwf = lambda: bmb.gemm(True, False, cout, cin, BT, 1.0, y.data_ptr(), x.data_ptr(),
-                               1.0, w.data_ptr())
+        dwf = lambda: bmb.gemm(True, False, cout, cin, BT, 1.0, DY.data_ptr(), X.data_ptr(),
+                               1.0, DW.data_ptr())
         reps = 3 if name == "lm_head" else 10
-        res[name] = {"shape": "%dx%dx%d" % (BT, cout, cin),
-                     "fwd_NT": gf(fl, timed_burst(fwd, reps)),
+        entry = {"shape": "%dx%dx%d" % (BT, cout, cin)}
+        rows_bt = sample_rows(BT, seed=3, extra=4)
+        rows_co = sample_rows(cout, seed=5, extra=4)
+        hXm, hDYm = hX.reshape(BT, cin), hDY.reshape(BT, cout)
+        for mname, math, ceil in modes:
+            with bmb.gemm_math(math):
+                fwd()
+                dxf()
+                DW.copy_(torch.from_numpy(hDW0))
+                dwf()
+                torch.cuda.synchronize()
+                bmb.check("gemm %s %s" % (name, mname))
+                tag = "config3 %s %s" % (name, mname)
+                V.gemm_rows(tag + " fwd_NT", Y.view(BT, cout)[rows_bt].cpu().numpy(),
+                            hXm[rows_bt], hW, True, cout, cin, 1.0, 0.0, None, mname, 1e-4)
+                V.gemm_rows(tag + " dX_NN", DX.view(BT, cin)[rows_bt].cpu().numpy(),
+                            hDYm[rows_bt], hW, False, cin, cout, 1.0, 0.0, None, mname, 1e-4)
+                V.gemm_rows(tag + " dW_TN_beta1", DW.view(cout, cin)[rows_co].cpu().numpy(),
+                            np.ascontiguousarray(hDYm[:, rows_co].T), hX, False, cin, BT, 1.0,
+                            1.0, hDW0.reshape(cout, cin)[rows_co], mname, 1e-4)
+                g = {"fwd_NT": gf(fl, timed_burst(fwd, reps)),
                      "dX_NN": gf(fl, timed_burst(dxf, reps)),
                      "dW_TN_beta1": gf(fl, timed_burst(dwf, reps))}
-        bmb.check("gemm " + name)
-        # Context only, not this build's result: the vendor's fp32 GEMM
-        # (hipBLASLt through torch, TF32 off) on the same operands.
-        X, Y = x[:BT * cin].view(BT, cin), y[:BT * cout].view(BT, cout)
-        W = w.view(cout, cin)
-        Yo, Xo = y[:BT * cout].view(BT, cout), x[:BT * cin].view(BT, cin)
-        res[name]["vendor_fp32"] = {
-            "fwd_NT": gf(fl, timed_burst(lambda: torch.matmul(X, W.t(), out=Yo), reps)),
-            "dX_NN": gf(fl, timed_burst(lambda: torch.matmul(Yo, W, out=Xo), reps)),
-            "dW_TN_beta1": gf(fl, timed_burst(lambda: W.addmm_(Yo.t(), Xo), reps))}
-        del x, w, y
+                bmb.check("gemm " + name)
+            g["pct_of_own_ceiling"] = {k: round(v / 1e3 / ceil * 100, 1) for k, v in g.items()}
+            entry[mname] = g
+        Xm, Wm = X.view(BT, cin), W.view(cout, cin)
+        Ym, DYm, DXm = Y.view(BT, cout), DY.view(BT, cout), DX.view(BT, cin)
+        entry["vendor_fp32"] = {
+            "fwd_NT": gf(fl, timed_burst(lambda: torch.matmul(Xm, Wm.t(), out=Ym), reps)),
+            "dX_NN": gf(fl, timed_burst(lambda: torch.matmul(DYm, Wm, out=DXm), reps)),
+            "dW_TN_beta1": gf(fl, timed_burst(lambda: Wm.addmm_(DYm.t(), Xm), reps))}
+        res[name] = entry
+        progress("config 3 %s verified and timed" % name)
+        del X, W, DY, Y, DX, DW, Xm, Wm, Ym, DYm, DXm
     torch.cuda.empty_cache()
     return res
 
@@ -607,13 +763,18 @@ def lr_at(step, warmup, total, lr_max):
     return lr_min + 0.5 * (lr_max - lr_min) * (1.0 + math.cos(math.pi * p))
 
 
-def gpt_step_bench(args, bmb, torch):
+def gpt_step_bench(args, bmb, torch, V, steps=None, warm=None, tag=None):
     """Config 5: one training step = gpt_forward + gpt_backward + global-norm
     clipping + AdamW (src/train_gpt.cu:395-460 at one rank), GPT-2 small,
     B=8, T=1024, random init N(0, 0.02) from gpt_init(1337), synthetic
     i.i.d. uniform token ids in [0, 50257) (a fresh batch every step). Timed
     on the host clock with the device synchronised at both ends; the step
-    itself blocks on the loss and the gradient norm, as the trainer's does."""
+    itself blocks on the loss and the gradient norm, as the trainer's does.
+    The linear layers run in gemm()'s current arithmetic mode (bf16x3 by
+    default; `tag` names another), attention on the default fp16x3 flash
+    kernels. Verified: every loss finite, the first within 1 nat of ln V
+    (uniform targets on near-uniform initial logits)."""
+    import math
     import numpy as np
     cfg = (1024, 50257, 50304, 12, 12, 768)
     B, T = 8, 1024
@@ -621,7 +782,8 @@ def gpt_step_bench(args, bmb, torch):
     m.init(1337)
     n_params = int(m.g.num_params)
     rng = np.random.default_rng(1337)
-    warm, steps = min(args.warmup, 3), args.steps
+    warm = min(args.warmup, 3) if warm is None else warm
+    steps = args.steps if steps is None else steps
     total = warm + steps
     batches = [(rng.integers(0, cfg[1], B * T).astype(np.int32),
                 rng.integers(0, cfg[1], B * T).astype(np.int32)) for _ in range(total)]
@@ -642,6 +804,8 @@ def gpt_step_bench(args, bmb, torch):
         losses.append(loss)
         norms.append(gn)
     bmb.check("gpt step")
+    progress("config 5 (%s) timed: %.2f ms/step" % (tag or "bf16x3 GEMM",
+                                                    sum(times[warm:]) / max(1, steps)))
 
     def more_steps():  # untimed training steps for the clock / power reading
         x, y = batches[0]
@@ -650,7 +814,8 @@ def gpt_step_bench(args, bmb, torch):
         g = L.grad_global_norm(m.g.grads_mem, n_params)
         L.adamw_update(m.g.params_mem, m.g.grads_mem, m.g.m_mem, m.g.v_mem, n_params, 1e-4,
                        0.9, 0.999, 1e-8, 0.1, total + 1, 1.0 / g if g > 1.0 else 1.0)
-    tel = sustained_telemetry(more_steps)
+    tel = sustained_telemetry(more_steps) if tag is None else {"available": False,
+                                                                "reason": "not measured"}
     # one more step split into its phases, for the breakdown
     x, y = batches[0]
     torch.cuda.synchronize()
@@ -671,13 +836,21 @@ def gpt_step_bench(args, bmb, torch):
     ms = sum(timed_ms) / len(timed_ms)
     hs = cfg[5] // cfg[4]
     flops = 6.0 * B * T * n_params + 12.0 * cfg[3] * cfg[4] * T * T * hs * B
+    lnv = math.log(cfg[1])
+    V.record("config5 %s losses finite, first within 1 nat of ln V" % (tag or "bf16x3 GEMM"),
+             abs(losses[0] - lnv) if all(math.isfinite(x) for x in losses) else float("inf"),
+             1.0, "|loss_first - ln V|; every loss finite")
+    gemm_kind = tag or "bf16x3 GEMM"
     return {
-        "metric": "GPT-2 small training step tokens/s (fp32, AdamW)",
+        "metric": "GPT-2 small training step tokens/s (%s + fp16x3 attention, fp32 AdamW)"
+                  % gemm_kind,
+        "compute": "fp32 in/out everywhere; linear layers on %s products (%s), attention on "
+                   "the default fp16x3 flash kernels, elementwise ops and AdamW in fp32"
+                   % (gemm_kind, "fp32 MFMA" if tag else "three bf16 MFMAs per fp32 product"),
         "value": round(B * T / (ms / 1e3), 1), "unit": "tokens/s",
         "ms_per_step": round(ms, 3), "ms_best": round(min(timed_ms), 3),
         "steps": steps, "warmup": warm,
         "tflops_train_gpt_accounting": round(flops / (ms / 1e3) / 1e12, 2),
-        "pct_fp32_peak": round(100 * flops / (ms / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 1),
         "phase_ms": {"forward": round((t1 - t0) * 1e3, 2), "backward": round((t2 - t1) * 1e3, 2),
                      "norm_clip_adamw": round((t3 - t2) * 1e3, 2)},
         "params": n_params,
@@ -692,7 +865,31 @@ def gpt_step_bench(args, bmb, torch):
     }
 
 
-def flash_bench(args, bmb, O, torch, traffic):
+def verify_flash(V, O, qkv, dout, out, lse, dqkv, dsum, Bf, T, C, NH):
+    """Batch 0 (12 heads) of one forward + backward against the fp64 oracle:
+    out, dq, dk, dv normwise (each within the reference's 1e-5,
+    tools/test_flash.cu:132,226,314), lse and dsum absolute / relative."""
+    import numpy as np
+    nb = 1
+    o = out.view(Bf, T, C)[:nb].cpu().numpy()
+    l = lse.view(Bf, NH, T)[:nb].cpu().numpy()
+    d = dqkv.view(Bf, T, 3 * C)[:nb].cpu().numpy()
+    ds = dsum.view(Bf, NH, T)[:nb].cpu().numpy()
+    ref_o, ref_l = O.attn_fwd_f64(qkv[:nb], nb, T, C, NH)
+    ref_d = O.attn_bwd_f64(qkv[:nb], dout[:nb], nb, T, C, NH)
+    ref_ds = O.dsum_f64(dout[:nb], o, nb, T, C, NH)
+    e, bad = O.normwise(o, ref_o)
+    V.record("flash out (batch 0)", e if not bad else float("inf"), 1e-5, "normwise vs fp64")
+    V.record("flash lse (batch 0)", float(np.abs(l - ref_l).max()), 1e-5, "max abs vs fp64")
+    V.record("flash dsum (batch 0)", float(np.abs(ds - ref_ds).max() / np.abs(ref_ds).max()),
+             1e-5, "max abs / max |ref| vs fp64")
+    for s_, name in enumerate("qkv"):
+        e, bad = O.normwise(d[:, :, s_ * C:(s_ + 1) * C], ref_d[:, :, s_ * C:(s_ + 1) * C])
+        V.record("flash d%s (batch 0)" % name, e if not bad else float("inf"), 1e-5,
+                 "normwise vs fp64")
+
+
+def flash_bench(args, bmb, O, torch, traffic, V):
     Bf, NH, T, hs = FLASH["B"], FLASH["NH"], FLASH["T"], FLASH["hs"]
     C = NH * hs
     qkv = O.fill_normal(Bf * T * 3 * C, 0xBEEF).reshape(Bf, T, 3 * C)
@@ -712,7 +909,11 @@ def flash_bench(args, bmb, O, torch, traffic):
         fwd()
         bwd()
 
-    fwd()
+    step()
+    torch.cuda.synchronize()
+    bmb.check("flash verification")
+    verify_flash(V, O, qkv, dout, out, lse, dqkv, dsum, Bf, T, C, NH)
+    progress("flash verified")
     tot, wall = timed_steps(step, args.steps, args.warmup, "flash")  # one step = fwd + bwd
     f_ms, _ = timed_steps(fwd, args.steps, 2)
     b_ms, _ = timed_steps(bwd, args.steps, 2)
@@ -723,7 +924,8 @@ def flash_bench(args, bmb, O, torch, traffic):
     fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
     tf = (fwd_fl + bwd_fl) / tot / 1e9
     flash = {
-        "metric": "flash fwd+bwd TFLOP/s @B=8,H=12,T=1024,d=64 (causal, fp32)",
+        "metric": "flash fwd+bwd TFLOP/s @B=8,H=12,T=1024,d=64 (causal, fp32 in/out, "
+                  "fp16x3 products)",
         "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(tot, 4),
         "ms_per_step_wall": round(wall, 4),
         "ms_fwd": round(f_ms, 4), "ms_bwd": round(b_ms, 4),
@@ -732,7 +934,6 @@ def flash_bench(args, bmb, O, torch, traffic):
         "independent_runs": runs,
         "tflops_fwd": round(fwd_fl / f_ms / 1e9, 2),
         "tflops_bwd": round(bwd_fl / b_ms / 1e9, 2),
-        "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_TFLOPS, 1),
         "fp16x3_ceiling_tflops": round(FP16X3_CEILING_TFLOPS, 1),
         "gflop_algorithmic": round((fwd_fl + bwd_fl) / 1e9, 2),
         "tflops_ref_accounting": round(4.5 * fwd_fl / tot / 1e9, 2),

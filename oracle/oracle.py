@@ -112,12 +112,20 @@ def bf16_rne(x) -> np.ndarray:
     return r.astype(np.uint32).view(np.float32)
 
 
+# The largest float that rounds to a finite bfloat16 (bits 0x7F7F7FFF).
+BF16_FINITE_MAX = float(np.array(0x7F7F7FFF, np.uint32).view(np.float32))
+
+
 def bf16x3_split(x):
-    """(hi, lo) of the bf16x3 scheme of KERNELS id 10: hi = bf16(x),
-    lo = bf16(x - hi); x - hi is exact in fp32 (hi holds x's leading bits)."""
+    """(hi, lo) of the bf16x3 scheme of KERNELS id 10 and gemm()
+    (csrc/sgemm_bf16x3.hip split4): hi = bf16(clamp(x, +-BF16_FINITE_MAX)),
+    lo = bf16(x - hi). x - hi is exact in fp32 for every finite x (hi holds
+    x's leading bits; above BF16_FINITE_MAX hi is bf16's largest finite
+    value, within a factor 2 of x); an infinite x gives (+-3.39e38, +-inf)."""
     x = _c(x)
-    hi = bf16_rne(x)
-    lo = bf16_rne(x - hi)
+    hi = bf16_rne(np.clip(x, np.float32(-BF16_FINITE_MAX), np.float32(BF16_FINITE_MAX)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        lo = bf16_rne(x - hi)
     return hi, lo
 
 

@@ -63,7 +63,7 @@ def test_unfused_attention_vs_oracle(gpu, shape):
     eo, bad = O.normwise(out, ref_o)
     assert bad == 0 and eo < TOL, eo
     ref_d = O.attn_bwd_f64(qkv, dout, B, T, C, NH)
-    errs = _check_grads(dqkv.reshape(B, T, 3 * C), ref_d, C)
+    errs = _check_grads(dqkv.reshape(B, T, 3 * C), ref_d, C, h16=False)
     print("out %.2e dq %.2e dk %.2e dv %.2e" % (eo, *errs))
     assert max(errs) < TOL
 

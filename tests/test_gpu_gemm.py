@@ -18,7 +18,7 @@ import pytest
 
 import bmb
 import oracle as O
-from gpu_util import Guarded, bf16x3_err, dev, sync
+from gpu_util import Guarded, bf16x3_err, dev, fp32_order_bound, sync
 
 pytestmark = pytest.mark.gpu
 
@@ -219,20 +219,183 @@ def test_split_k(gpu, shape, trans):
 
 
 def test_non_null_stream_matches(gpu):
-    """On a stream other than the null stream gemm() does not split K (its
-    scratch is ordered by the null stream only); the result agrees with the
-    oracle all the same."""
+    """gemm() splits K on any stream: its scratch is leased per call and its
+    reuse is ordered by an event on the caller's stream. 768 x 768 x 8192 TN
+    (the GPT-2 attention-projection dW, split into several K ranges) on a
+    torch side stream gives the null stream's bits, twice in a row (the
+    second call reuses the first call's buffer), and both are within the
+    bf16x3 bound."""
     import torch
-    M, N, K = 384, 384, 4096
+    M, N, K = 768, 768, 8192
     A = O.fill_xorshift(M * K, 0x1111)
     B = O.fill_xorshift(K * N, 0x2222)
     C0 = O.fill_xorshift(M * N, 0x3333)
-    dA, dB, dC = dev(A), dev(B), dev(C0)
+    dA, dB, dC0 = dev(A), dev(B), dev(C0)
+    dC = dC0.clone()
+    bmb.gemm(True, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr())
+    sync("gemm on the null stream")
+    ref = dC.cpu().numpy().view(np.uint32).copy()
     s = torch.cuda.Stream()
-    with torch.cuda.stream(s):
-        bmb.gemm(True, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr(),
-                 s.cuda_stream)
-    s.synchronize()
-    bmb.check("gemm on stream")
-    e3, bound = bf16x3_err(dC.cpu().numpy(), True, False, M, N, K, 1.0, A, B, 0.5, C0)
+    for i in range(2):
+        print("gemm TN %dx%dx%d on a side stream, call %d" % (M, N, K, i), flush=True)
+        with torch.cuda.stream(s):
+            dC.copy_(dC0)
+            bmb.gemm(True, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5,
+                     dC.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        bmb.check("gemm on stream")
+        got = dC.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref)
+    e3, bound = bf16x3_err(got, True, False, M, N, K, 1.0, A, B, 0.5, C0)
     assert e3 < bound, (e3, bound)
+
+
+def test_two_streams_share_scratch_in_order(gpu):
+    """Two streams that each run split-K gemm() calls back to back, with no
+    ordering between the streams: every call leases the partials buffer the
+    other stream's last call returned, so each lease must wait for that
+    call's kernels. Each result equals its null-stream bits."""
+    import torch
+    shapes = [(768, 768, 8192, True), (768, 3072, 8192, True)]
+    data = []
+    for i, (M, N, K, ta) in enumerate(shapes):
+        A = O.fill_xorshift(M * K, 0x7070 + i)
+        B = O.fill_xorshift(K * N, 0x8080 + i)
+        d = {"A": dev(A), "B": dev(B), "shape": (M, N, K, ta)}
+        d["C"] = torch.empty(M * N, device="cuda", dtype=torch.float32)
+        bmb.gemm(ta, False, M, N, K, 1.0, d["A"].data_ptr(), d["B"].data_ptr(), 0.0,
+                 d["C"].data_ptr())
+        sync("reference gemm")
+        d["ref"] = d["C"].cpu().numpy().view(np.uint32).copy()
+        d["outs"] = [torch.empty(M * N, device="cuda", dtype=torch.float32) for _ in range(4)]
+        data.append(d)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    print("two streams x 4 split-K gemm() calls", flush=True)
+    for r in range(4):
+        for d, s in zip(data, streams):
+            M, N, K, ta = d["shape"]
+            bmb.gemm(ta, False, M, N, K, 1.0, d["A"].data_ptr(), d["B"].data_ptr(), 0.0,
+                     d["outs"][r].data_ptr(), s.cuda_stream)
+    torch.cuda.synchronize()
+    bmb.check("gemm on two streams")
+    for d in data:
+        for o in d["outs"]:
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), d["ref"])
+
+
+# ---- gemm_set_math(GEMM_MATH_FP32): fp32 matrix-core products, held to the
+# fp32 summation bound (the rounding level of the reference's fp32 gemm()).
+
+@pytest.fixture
+def fp32_math(gpu):
+    with bmb.gemm_math(bmb.GEMM_MATH_FP32):
+        assert bmb.gemm_get_math() == bmb.GEMM_MATH_FP32
+        yield
+    assert bmb.gemm_get_math() == bmb.GEMM_MATH_BF16X3
+
+
+def test_math_switch_rejects_unknown_modes(gpu):
+    assert bmb.gemm_get_math() == bmb.GEMM_MATH_BF16X3
+    assert bmb.gemm_set_math(7) == -1
+    assert bmb.gemm_get_math() == bmb.GEMM_MATH_BF16X3
+
+
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("shape", SHAPES + SPLIT[:3], ids=lambda s: "%dx%dx%d" % s)
+def test_fp32_math_shapes(fp32_math, shape, trans):
+    """The reference's 10 shapes x 4 transposes (tools/test_gemm.cu:51-62)
+    and three split-K shapes in fp32 mode: within fp32_order_bound(K) of the
+    fp64 product, which the bf16x3 default (~1e-6) would miss at every K."""
+    M, N, K = shape
+    ta, tb = trans
+    A = O.fill_xorshift(M * K, 0x1234)
+    B = O.fill_xorshift(K * N, 0x9ABC)
+    C0 = O.fill_xorshift(M * N, 0x5555)
+    dA, dB = dev(A), dev(B)
+    gC = Guarded(M * N, fill=C0)
+    print("gemm fp32 %s M=%d N=%d K=%d" % (_tag(trans), M, N, K), flush=True)
+    bmb.gemm(ta, tb, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 1.25, gC.ptr)
+    sync("gemm fp32")
+    assert gC.ok()
+    err, bad = O.normwise(gC.get(), O.gemm_f64(ta, tb, M, N, K, 0.75, A, B, 1.25, C0))
+    print("  normwise %.2e (bound %.2e)" % (err, fp32_order_bound(K)))
+    assert bad == 0 and err < fp32_order_bound(K)
+
+
+@pytest.mark.parametrize("g", GPT, ids=lambda g: "%dx%dx%d_%s" % (g[0], g[1], g[2], _tag(g[3:5])))
+def test_fp32_math_gpt_training_shapes(fp32_math, g):
+    """BASELINE config 3 at the reference's arithmetic: the 15 GPT-2 GEMMs in
+    fp32 mode, row-sampled against fp64, within fp32_order_bound(K)."""
+    import torch
+    M, N, K, ta, tb, beta = g
+    A = O.fill_normal(M * K, 0xA11CE, 1.0)
+    B = O.fill_normal(K * N, 0xB0B, 0.02)
+    C0 = O.fill_normal(M * N, 0xC0C0, 1.0) if beta != 0 else None
+    dA, dB = dev(A), dev(B)
+    dC = dev(C0) if C0 is not None else torch.empty(M * N, device="cuda", dtype=torch.float32)
+    print("gpt gemm fp32 %s M=%d N=%d K=%d beta=%g" % (_tag((ta, tb)), M, N, K, beta), flush=True)
+    bmb.gemm(ta, tb, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), beta, dC.data_ptr())
+    sync("gemm fp32")
+    got = dC.cpu().numpy().reshape(M, N)
+    rows = np.unique(np.r_[0, 1, 255, 256, M // 2, M - 1, np.random.default_rng(4).integers(0, M, 6)])
+    Aop = (A.reshape(K, M).T if ta else A.reshape(M, K))[rows]
+    c0 = C0.reshape(M, N)[rows] if C0 is not None else None
+    ref = O.gemm_f64(False, tb, len(rows), N, K, 1.0, np.ascontiguousarray(Aop), B, beta, c0)
+    err, bad = O.normwise(got[rows], ref)
+    print("  normwise %.2e (bound %.2e)" % (err, fp32_order_bound(K)))
+    assert bad == 0 and err < fp32_order_bound(K)
+
+
+# ---- the top of the fp32 range and infinities (both modes)
+
+@pytest.mark.parametrize("math", [0, 1], ids=["bf16x3", "fp32"])
+def test_top_of_range_and_infinities(gpu, math):
+    """Finite entries of A up to FLT_MAX (above 0x7F7F7FFF, where a plain
+    bfloat16 rounding would give infinity) with B on a 1e-3 scale: the
+    result is finite and within the mode's bound of the fp64 product (for
+    bf16x3: around the split's exact value). Rows of A holding one +-inf
+    each: every entry of such a row is +-inf with the sign of inf * b, or
+    NaN where b = 0 (fp32 semantics); the other rows are unaffected."""
+    import torch
+    M, N, K = 192, 160, 96
+    A = O.fill_xorshift(M * K, 0xF00D).reshape(M, K)
+    B = (O.fill_xorshift(K * N, 0xBEEF) * np.float32(1e-3)).reshape(K, N)
+    big = np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0xFF7F8001, 0x7F7F7FFF, 0x7F700000],
+                   np.uint32).view(np.float32)
+    r = np.random.default_rng(5)
+    A[r.integers(0, M, 40), r.integers(0, K, 40)] = r.choice(big, 40)
+    with bmb.gemm_math(math):
+        dA, dB = dev(A), dev(B)
+        dC = torch.empty(M * N, device="cuda", dtype=torch.float32)
+        print("gemm top of range, math %d" % math, flush=True)
+        bmb.gemm(False, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.0, dC.data_ptr())
+        sync("gemm top of range")
+        got = dC.cpu().numpy().reshape(M, N)
+        assert np.isfinite(got).all()
+        err, _ = O.normwise(got, O.gemm_f64(False, False, M, N, K, 1.0, A, B, 0.0, None))
+        if math == 0:
+            e3, bound = bf16x3_err(got, False, False, M, N, K, 1.0, A, B, 0.0, None)
+            assert e3 < bound, (e3, bound)
+            assert err < 1e-4
+        else:
+            assert err < fp32_order_bound(K), err
+        # infinities: rows 3 and 70 get +inf and -inf
+        Ai = A.copy()
+        Ai[3, 17], Ai[70, 5] = np.inf, -np.inf
+        B0 = B.copy()
+        B0[17, :7] = 0.0  # inf * 0 = NaN in those entries of row 3
+        dA, dB = dev(Ai), dev(B0)
+        bmb.gemm(False, False, M, N, K, 1.0, dA.data_ptr(), dB.data_ptr(), 0.0, dC.data_ptr())
+        sync("gemm infinities")
+        got = dC.cpu().numpy().reshape(M, N)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = Ai.astype(np.float64) @ B0.astype(np.float64)
+    for i in (3, 70):
+        assert np.array_equal(np.isnan(got[i]), np.isnan(want[i]))
+        fin = ~np.isnan(want[i])
+        assert np.isinf(got[i][fin]).all()
+        assert np.array_equal(np.sign(got[i][fin]), np.sign(want[i][fin]))
+    assert np.isnan(got[3, :7]).all()
+    rest = np.setdiff1d(np.arange(M), [3, 70])
+    assert np.isfinite(got[rest]).all()

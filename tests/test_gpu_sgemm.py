@@ -124,6 +124,49 @@ def test_large_sampled_rows(gpu, kid, n):
 
 
 @pytest.mark.parametrize("kid", VALU_IDS + MFMA_IDS)
+def test_config1_exact_call(gpu, kid):
+    """BASELINE config 1 as the bench times it: N = 1024, alpha = 1, beta = 0
+    (C write-only, so it starts as NaN here), the bench's seeds. Its bar is
+    normwise 1e-6 against the CPU triple loop, whose fp32 restatement is the
+    oracle's sequential fmaf: ids 1-8 equal it bit for bit (error 0). The
+    triple loop is itself ~1.5e-6 from the exact product here, so the matrix
+    paths, whose summation order differs, are held to their own bounds
+    around fp64 instead: id 9 to the fp32 summation bound, id 10 to the
+    bf16x3 bound (its split alone is 3.6e-6 from the exact product)."""
+    n = 1024
+    A, B, _ = _inputs(n, n, n)
+    got = _run(kid, n, n, n, 1.0, 0.0, A, B, np.full((n, n), np.nan, np.float32))
+    assert np.isfinite(got).all()
+    seq = O.gemm_f32seq(0, 0, n, n, n, 1.0, A, B, 0.0, None, threads=0)
+    ref = O.gemm_f64(0, 0, n, n, n, 1.0, A, B, 0.0, None)
+    err, _ = O.normwise(got, ref)
+    e_seq = O.normwise(got, seq)[0]
+    print("config 1, id %d: normwise %.2e vs fp64, %.2e vs the CPU triple loop (which is "
+          "%.2e from fp64)" % (kid, err, e_seq, O.normwise(seq, ref)[0]))
+    assert err < bmb.find_kernel(kid)["tol"]
+    if kid in VALU_IDS:
+        assert np.array_equal(got, seq) and e_seq <= 1e-6
+    elif kid == 9:
+        assert err < fp32_order_bound(n)
+    else:
+        _check_bf16x3(got, n, n, n, 1.0, A, B, 0.0, None)
+
+
+@pytest.mark.parametrize("kid", [1, 2, 3, 4, 5, 6, 7])
+def test_ladder_at_bench_size(gpu, kid):
+    """The ladder's fp32 VALU stages at N = 4096 (alpha 1, beta 0.5, C
+    pre-filled: the size and call bench.py times them at), bit-exact against
+    the sequential-fmaf oracle on a row sample (rows are independent)."""
+    n = 4096
+    A, B, C0 = _inputs(n, n, n)
+    got = _run(kid, n, n, n, 1.0, 0.5, A, B, C0)
+    rows = np.unique(np.r_[0, 1, 31, 32, 127, 128, n // 2, n - 33, n - 1,
+                           np.random.default_rng(11).integers(0, n, 6)])
+    want = O.gemm_f32seq(0, 0, len(rows), n, n, 1.0, A[rows], B, 0.5, C0[rows], threads=0)
+    assert np.array_equal(got[rows], want)
+
+
+@pytest.mark.parametrize("kid", VALU_IDS + MFMA_IDS)
 def test_beta_zero_is_write_only(gpu, kid):
     """beta == 0 never reads C: a NaN-filled C gives alpha*A@B."""
     M, N, K = 130, 200, 48

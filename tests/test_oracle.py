@@ -344,3 +344,24 @@ def test_bf16_rne_matches_torch():
     assert np.array_equal((x - hi) + hi, x)  # x - hi is exact in fp32
     big = np.abs(x) > 1e-30
     assert (np.abs(x - hi - lo)[big] <= np.abs(x)[big] * 2.0 ** -16).all()
+
+
+def test_bf16x3_split_at_the_top_of_the_range():
+    """Finite values that round to a bfloat16 infinity (|x| > 0x7F7F7FFF, up
+    to FLT_MAX) still split exactly: hi is bf16's largest finite value with
+    x's sign, x - hi is exact, and hi + lo is within 2^-16 |x|; at the
+    threshold itself hi is x rounded as usual. An infinite x splits into
+    (+-0x7F7F, +-inf)."""
+    t = np.array([0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF, 0x7F7F0000, 0xFF7FFFFF, 0xFF7F8001],
+                 np.uint32).view(np.float32)
+    hi, lo = O.bf16x3_split(t)
+    assert np.isfinite(hi).all() and np.isfinite(lo).all()
+    assert (np.abs(hi).view(np.uint32) == 0x7F7F0000).all()
+    assert np.array_equal((t - hi) + hi, t)
+    assert (np.abs(t.astype(np.float64) - hi - lo) <= np.abs(t) * 2.0 ** -16).all()
+    # below the threshold nothing changed: plain round to nearest even
+    assert O.bf16_rne(t[:1])[0] == hi[0] and O.BF16_FINITE_MAX == float(t[0])
+    inf = np.array([np.inf, -np.inf], np.float32)
+    hi, lo = O.bf16x3_split(inf)
+    assert (np.abs(hi).view(np.uint32) == 0x7F7F0000).all() and np.array_equal(lo, inf)
+    assert np.array_equal(np.sign(hi), np.sign(inf))
