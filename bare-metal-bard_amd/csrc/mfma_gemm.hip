@@ -12,8 +12,10 @@
 
 #include <algorithm>
 #include <atomic>
+#include <map>
 #include <mutex>
 #include <optional>
+#include <tuple>
 
 #include "mfma_gemm.hpp"
 #include "../../include/gemm.h"
@@ -79,6 +81,14 @@ constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last rou
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
 constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
+// A second band: its launch and the drain between the bands. Bands are only
+// tried for K >= MIN_BAND_K, with K ranges of at least MIN_BAND_SPLIT_K in a
+// split remainder band, and taken when modelled 3% faster than one band (as
+// in the bf16x3 planner, sgemm_bf16x3.hip, where these bounds were measured).
+constexpr double BAND_S = 12.0e-6;
+constexpr double BAND_GAIN = 0.97;
+constexpr int MIN_BAND_K = 4096;
+constexpr int MIN_BAND_SPLIT_K = 512;
 // Largest split-K partial buffer (floats): 640 MiB per call in flight on a device.
 constexpr long long MAX_SPLIT_FLOATS = 160LL << 20;
 
@@ -146,10 +156,22 @@ void tile_occupancy(int (&out)[2]) {
     out[1] = wgs_per_cu(bmb::mfma_gemm_splitk_k<TA, TB, Tile, VEC>, Tile::NT, L::SMEM_BYTES);
 }
 
+// One band's launch: tile candidate, K ranges (1: no split) and the K per
+// range (a multiple of 16).
+struct Part {
+    int tile;
+    int splits;
+    int kchunk;
+};
+
+// Rows [0, m1) run on part[0], rows [m1, M) on part[1] (m1 == M: one band).
+// As in the bf16x3 planner (sgemm_bf16x3.hip), a tile count just above a
+// whole number of rounds (4097^2 on 256 x 256: 289 tiles on 256 CUs) is run
+// as a first band of whole rounds and a remainder band on its own tile and
+// split, one launch after the other on the same stream.
 struct Plan {
-    Cand tile;
-    int splits;  // number of K ranges (1: no split)
-    int kchunk;  // K per range, a multiple of 16
+    Part part[2];
+    int m1;
 };
 
 inline int round_up16(long long x) { return (int)((x + 15) / 16 * 16); }
@@ -173,13 +195,13 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     return t;
 }
 
-// Split-K is used only for single problems (KERNELS id 9, gemm() in fp32
-// mode; batched_gemm() never splits). max_floats caps the partials
-// (splits * M * N).
-Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
-          long long max_floats = MAX_SPLIT_FLOATS) {
-    const int cus = device_cus();
-    Plan best{CANDS[0], 1, round_up16(K)};
+// The fastest single-band plan (tile, split) of an M x N x K band, and its
+// modelled time. Split-K is used only for single problems (KERNELS id 9,
+// gemm() in fp32 mode; batched_gemm() never splits); max_floats caps the
+// partials (splits * M * N).
+double best_part(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
+                 long long max_floats, int cus, Part &best, int min_split_k = 0) {
+    best = Part{0, 1, round_up16(K)};
     double best_t = -1.0;
     for (int ci = 0; ci < N_CANDS; ++ci) {
         const Cand &c = CANDS[ci];
@@ -191,16 +213,71 @@ Plan pick(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
                 if (splits < 2 || (long long)splits * M * N > max_floats) continue;
+                if (kchunk < min_split_k) continue;
             }
             const double t =
                 model_time(M, N, K, batch, c, occ.wgs[ci][splits > 1], splits, kchunk, cus);
             if (best_t < 0 || t < best_t) {
                 best_t = t;
-                best = Plan{c, splits, kchunk};
+                best = Part{ci, splits, kchunk};
+            }
+        }
+    }
+    return best_t;
+}
+
+Plan plan_for(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
+              long long max_floats) {
+    const int cus = device_cus();
+    Plan best{{Part{0, 1, round_up16(K)}, Part{0, 1, round_up16(K)}}, M};
+    const double single_t = best_part(M, N, K, batch, may_split, occ, max_floats, cus,
+                                      best.part[0]);
+    if (batch != 1 || K < MIN_BAND_K) return best;
+    double best_t = single_t;
+    for (int ci = 0; ci < N_CANDS; ++ci) {
+        const Cand &c = CANDS[ci];
+        const long long tiles_n = (N + c.bn - 1) / c.bn;
+        const long long slots = (long long)cus * occ.wgs[ci][0];
+        for (long long k = 1;; ++k) {
+            const long long rows = k * slots / tiles_n;  // tile rows in k whole rounds
+            if (rows <= 0) continue;
+            if (rows * c.bm >= M) break;
+            const int m1 = (int)(rows * c.bm);
+            const double t0 = model_time(m1, N, K, 1, c, occ.wgs[ci][0], 1, round_up16(K), cus);
+            Part p1;
+            const double t1 =
+                best_part(M - m1, N, K, 1, may_split, occ, max_floats, cus, p1, MIN_BAND_SPLIT_K);
+            if (t1 < 0) continue;
+            const double tm = t0 + t1 + BAND_S;
+            if (tm < BAND_GAIN * single_t && tm < best_t) {
+                best_t = tm;
+                best = Plan{{Part{ci, 1, round_up16(K)}, p1}, m1};
             }
         }
     }
     return best;
+}
+
+// Plans memoised per (device, case, shape, batch, split permission and cap).
+template <bool TA, bool TB, int EPI>
+Plan pick(int M, int N, int K, int batch, bool vec, bool may_split, const Occupancy &occ,
+          long long max_floats = MAX_SPLIT_FLOATS) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    using Key = std::tuple<int, bool, int, int, int, int, bool, long long>;
+    static std::mutex mu;
+    static std::map<Key, Plan> memo;
+    const Key key{dev, vec, M, N, K, batch, may_split, max_floats};
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = memo.find(key);
+        if (it != memo.end()) return it->second;
+    }
+    const Plan p = plan_for(M, N, K, batch, may_split, occ, max_floats);
+    std::lock_guard<std::mutex> lock(mu);
+    if (memo.size() > 4096) memo.clear();
+    memo.emplace(key, p);
+    return p;
 }
 
 // The occupancy table of one (transposes, epilogue, alignment) case, queried
@@ -229,7 +306,7 @@ const Occupancy &occupancy(bool vec) {
 }
 
 template <bool TA, bool TB, class Tile, int EPI>
-void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
+void launch_tile(int batch, int M, int N, int K, float alpha, const float *A, int lda,
                  long long sA, const float *B, long long sB, float beta,
                  float *C, long long sC, hipStream_t stream, bool vec, bmb::EpiArgs ep) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
@@ -238,12 +315,12 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
     if (vec) {
         bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
+                    L::SMEM_BYTES, stream, M, N, K, alpha, A, lda, sA, B, sB, beta, C,
                     sC, tiles_m, tiles_n, ep);
     } else {
         bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, alpha, A, sA, B, sB, beta, C,
+                    L::SMEM_BYTES, stream, M, N, K, alpha, A, lda, sA, B, sB, beta, C,
                     sC, tiles_m, tiles_n, ep);
     }
 }
@@ -251,7 +328,7 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A,
 // Split-K: the partial sums of each K range go to P (splits x M x N), then
 // one reduce kernel adds them in range order and applies the epilogue.
 template <bool TA, bool TB, class Tile, int EPI>
-void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *A,
+void launch_split(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
                   const float *B, float beta, float *C, float *P, bool vec, bmb::EpiArgs ep,
                   hipStream_t stream) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
@@ -260,22 +337,53 @@ void launch_split(const Plan &p, int M, int N, int K, float alpha, const float *
     if (vec) {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, A, lda, B, P, tiles_m, tiles_n, p.kchunk);
     } else {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, A, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, A, lda, B, P, tiles_m, tiles_n, p.kchunk);
     }
     const long long mn = (long long)M * N;
     bmb::launch(bmb::splitk_reduce_k<EPI>, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
                 stream, C, (const float *)P, p.splits, mn, N, alpha, beta, ep);
 }
 
+template <bool TA, bool TB, int EPI>
+void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const float *A,
+              int lda, long long sA, const float *B, long long sB, float beta, float *C,
+              long long sC, float *P, bool vec, bmb::EpiArgs ep, hipStream_t stream) {
+    if (p.splits > 1) {
+        switch (CANDS[p.tile].kind) {
+        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        }
+        return;
+    }
+    switch (CANDS[p.tile].kind) {
+    case TileKind::L:
+        launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
+        break;
+    case TileKind::M:
+        launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
+        break;
+    case TileKind::N:
+        launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
+        break;
+    case TileKind::S:
+        launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
+        break;
+    }
+}
+
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Split-K partials go to `fixed` (at most fixed_floats), or else to scratch
 // leased for `stream` (reuse ordered by the lease's event); under graph
-// capture, where a lease could allocate, K is not split.
+// capture, where a lease could allocate, K is not split. The bands of a plan
+// run in row order on the stream; a second band's split partials reuse P
+// after the first band's reduce has read it.
 template <bool TA, bool TB, int EPI = bmb::EPI_BLAS>
 void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
               long long sA, const float *B, long long sB, float beta, float *C,
@@ -290,37 +398,31 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
                      (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
     const Occupancy &occ = occupancy<TA, TB, EPI>(vec);
     const bool may_split = batch == 1 && (fixed != nullptr || !bmb::stream_capturing(stream));
-    Plan p = pick(M, N, K, batch, may_split, occ, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
+    Plan p = pick<TA, TB, EPI>(M, N, K, batch, vec, may_split, occ,
+                               fixed ? fixed_floats : MAX_SPLIT_FLOATS);
+    long long pf = 0;
+    if (p.part[0].splits > 1) pf = (long long)p.part[0].splits * p.m1 * N;
+    if (p.m1 < M && p.part[1].splits > 1)
+        pf = std::max(pf, (long long)p.part[1].splits * (M - p.m1) * N);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1 && fixed == nullptr) {
-        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float), stream);
+    if (pf > 0 && fixed == nullptr) {
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)pf * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
-        if (P == nullptr) p = pick(M, N, K, batch, false, occ);  // no scratch: no split
+        if (P == nullptr) p = pick<TA, TB, EPI>(M, N, K, batch, vec, false, occ);  // no split
     }
-    if (p.splits > 1) {
-        switch (p.tile.kind) {
-        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, B, beta, C, P, vec, ep, stream); break;
-        }
-        return;
-    }
-    switch (p.tile.kind) {
-    case TileKind::L:
-        launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::M:
-        launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::N:
-        launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::S:
-        launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    }
+    const int lda = TA ? M : K;
+    run_band<TA, TB, EPI>(p.part[0], batch, p.m1, N, K, alpha, A, lda, sA, B, sB, beta, C, sC,
+                          P, vec, ep, stream);
+    if (p.m1 >= M) return;
+    const size_t r = (size_t)p.m1;
+    bmb::EpiArgs e1 = ep;
+    if (e1.act) e1.act += r * N;
+    if (e1.pre) e1.pre += r * N;
+    // A band of rows starts r rows (TA: r columns of the stored K x M) in.
+    const float *A1 = TA ? A + r : A + r * K;
+    run_band<TA, TB, EPI>(p.part[1], 1, M - p.m1, N, K, alpha, A1, lda, sA, B, sB, beta,
+                          C + r * N, sC, P, vec && al16(A1), e1, stream);
 }
 
 void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,

@@ -480,17 +480,20 @@ struct MfmaGemm {
 };
 
 // Grid: x = output tiles (XCD-remapped, grouped), y = batch index. The
-// fused epilogues (EPI_BIAS*) are used for single problems only.
+// fused epilogues (EPI_BIAS*) are used for single problems only. lda: A's
+// row stride (at least M when TA, K otherwise), so that a band of rows of a
+// larger problem (A offset to its first row) runs as its own problem; B and
+// C are whole rows (ldb from K and N, C packed).
 template <bool TA, bool TB, class Tile, bool VEC, int EPI>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
-    int M, int N, int K, float alpha, const float *__restrict__ A,
+    int M, int N, int K, float alpha, const float *__restrict__ A, int lda,
     long long sA, const float *__restrict__ B, long long sB, float beta,
     float *C, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
     extern __shared__ float smem_dyn[];
     const size_t z = blockIdx.y;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, TA ? M : K, TB ? K : N, alpha,
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, lda, TB ? K : N, alpha,
                                                    A + z * sA, B + z * sB, beta, C + z * sC,
                                                    tm * Tile::BM, tn * Tile::BN, smem_dyn, ep);
 }
@@ -501,7 +504,7 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
 // partial P + s*M*N; splitk_reduce_k then adds the splits in order.
 template <bool TA, bool TB, class Tile, bool VEC>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
-    int M, int N, int K, const float *__restrict__ A, const float *__restrict__ B,
+    int M, int N, int K, const float *__restrict__ A, int lda, const float *__restrict__ B,
     float *P, int tiles_m, int tiles_n, int kchunk) {
     extern __shared__ float smem_dyn[];
     const int s = blockIdx.y;
@@ -509,10 +512,10 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
     const int klen = min(K, kb + kchunk) - kb;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    const float *As = TA ? A + (size_t)kb * M : A + kb;
+    const float *As = TA ? A + (size_t)kb * lda : A + kb;
     const float *Bs = TB ? B + kb : B + (size_t)kb * N;
     MfmaGemm<TA, TB, Tile, VEC>::template run<EPI_PARTIAL>(
-        M, N, klen, TA ? M : K, TB ? K : N, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N,
+        M, N, klen, lda, TB ? K : N, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N,
         tm * Tile::BM, tn * Tile::BN, smem_dyn);
 }
 

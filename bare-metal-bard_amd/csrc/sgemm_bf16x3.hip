@@ -49,8 +49,11 @@
 // order is 1-5% faster on the GPT-2 shapes and 2% at N = 4096, bit-identical.
 #include <math.h>
 
+#include <algorithm>
+#include <map>
 #include <mutex>
 #include <optional>
+#include <tuple>
 #include <type_traits>
 
 #include "common.hpp"
@@ -550,9 +553,12 @@ struct Bf16x3Gemm {
 // Grid: x = output tiles (XCD-remapped, grouped), y = K range s, covering
 // k in [s*kchunk, min(K, (s+1)*kchunk)) (kchunk a multiple of BK when
 // gridDim.y > 1). EPI_PARTIAL: write the range's raw sums to C + s*M*N.
+// lda: A's row stride (at least M when TA, K otherwise), so that a band of
+// rows of a larger problem (A offset to its first row) runs as its own
+// problem; B and C are whole rows (ldb from K and N, C packed).
 template <class Tl, bool TA, bool TB, bool VEC, int EPI>
 __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchunk, float alpha,
-                                                   const float *__restrict__ A,
+                                                   const float *__restrict__ A, int lda,
                                                    const float *__restrict__ B, float beta,
                                                    float *C, int tiles_m, int tiles_n,
                                                    bmb::EpiArgs ep) {
@@ -561,7 +567,7 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
     int tm, tn;
     bmb::group_tile(bmb::xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const int m0 = tm * Tl::BM, n0 = tn * Tl::BN;
-    const int lda = TA ? M : K, ldb = TB ? K : N;
+    const int ldb = TB ? K : N;
     const int kb = blockIdx.y * kchunk, klen = min(K, kb + kchunk) - kb;
     const float *Ak = TA ? A + (size_t)kb * lda : A + kb;
     const float *Bk = TB ? B + kb : B + (size_t)kb * ldb;
@@ -587,6 +593,15 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // of them but N = 2048 (5%). The 128 x 256 tile serves the N = 768 and
 // 3072-wide GPT-2 layers with K = 768 or 3072 (4-9% faster than 128 x 128
 // there); a 256 x 128 tile was never chosen and is not built.
+//
+// Row bands. A tile count just above a whole number of rounds (4097^2 on
+// 256 x 256: 289 tiles on 256 CUs; 6144^2: 576 tiles, 2.25 rounds; the GPT-2
+// QKV forward, 8192 x 2304: 288 tiles) leaves most CUs idle for a whole
+// extra tile time. A plan may therefore run C as two bands of full-width
+// rows, one launch each on the same stream: rows [0, m1) on one tile with
+// whole K, sized to whole rounds, and rows [m1, M) on the plan (tile and
+// split) that suits that remainder, typically a smaller tile or a K split
+// that spreads it over every CU.
 struct B3Cand {
     int bm, bn;
     double tflops;  // fitted fp32-equivalent TFLOP/s when the device is full of them
@@ -606,6 +621,17 @@ constexpr double FILL_EXP = 0.3;
 constexpr double K_OVERHEAD = 96.0;               // per-item prologue/epilogue, in k
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;               // the reduce launch
+// A second band: its launch and the drain between the bands. Bands are only
+// tried for K >= MIN_BAND_K, with K ranges of at least MIN_BAND_SPLIT_K in a
+// split remainder band, and taken when modelled 3% faster than one band:
+// measured on MI355X, bands gained 15-18% at N = 4097 and 6144 and on the
+// GPT-2 LM-head weight gradient (K = 8192) and lost 3-7% on the K = 768 and
+// 3072 GPT-2 GEMMs of about 100 us, whose short K ranges the model
+// undercharges.
+constexpr double BAND_S = 12.0e-6;
+constexpr double BAND_GAIN = 0.97;
+constexpr int MIN_BAND_K = 4096;
+constexpr int MIN_BAND_SPLIT_K = 512;
 constexpr int MIN_SPLIT_K = 64;  // two stages
 constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;  // 256 MiB of partials
 
@@ -622,73 +648,149 @@ int occupancy_of() {
     return n < 1 ? 1 : n;
 }
 
-struct Plan {
+// One band's launch: tile candidate, K ranges and the K per range.
+struct Part {
     int tile, splits, kchunk;
 };
 
-// may_split: split-K partials have somewhere to go; max_floats caps them
-// (splits * M * N).
-Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
+// Rows [0, m1) run on part[0], rows [m1, M) on part[1] (m1 == M: one band).
+struct Plan {
+    Part part[2];
+    int m1;
+};
+
+struct Device {
+    int occ[N_CANDS], cus;
+};
+
+const Device &device_info(int dev) {
     static std::once_flag once[64];
-    static int occ[64][N_CANDS], cus[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    static Device info[64];
     std::call_once(once[dev], [&] {
-        occ[dev][0] = occupancy_of<TileL>();
-        occ[dev][1] = occupancy_of<TileM>();
-        occ[dev][2] = occupancy_of<TileS>();
-        occ[dev][3] = occupancy_of<TileT>();
+        Device &d = info[dev];
+        d.occ[0] = occupancy_of<TileL>();
+        d.occ[1] = occupancy_of<TileM>();
+        d.occ[2] = occupancy_of<TileS>();
+        d.occ[3] = occupancy_of<TileT>();
         int c = 0;
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             c <= 0) {
             (void)hipGetLastError();
             c = 256;
         }
-        cus[dev] = c;
+        d.cus = c;
     });
-    Plan best{0, 1, K};
+    return info[dev];
+}
+
+// Modelled time of an M x N x K band on tile t with K split s ways; false if
+// that split is not allowed (may_split, max_floats caps splits * M * N).
+bool part_time(const Device &dv, int M, int N, int K, int t, int s, bool may_split,
+               long long max_floats, Part &out, double &time) {
+    const B3Cand &c = CANDS[t];
+    int splits = 1, kchunk = K;
+    if (s > 1) {
+        if (!may_split || K < 2 * MIN_SPLIT_K) return false;
+        kchunk = (K + s - 1) / s;
+        kchunk = (kchunk + BK - 1) / BK * BK;
+        if (kchunk < MIN_SPLIT_K) return false;
+        splits = (K + kchunk - 1) / kchunk;
+        if (splits < 2 || (long long)splits * M * N > max_floats) return false;
+        if ((s & (s - 1)) != 0 && kchunk < MIN_ODD_SPLIT_K) return false;
+    }
+    const long long tiles = (long long)bmb::ceil_div(M, c.bm) * bmb::ceil_div(N, c.bn);
+    const long long items = tiles * splits;
+    const int occ = dv.occ[t], cus = dv.cus;
+    const long long slots = (long long)cus * occ;
+    const double t_item =
+        2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) * occ / (c.tflops * 1e12 / cus);
+    const long long full = items / slots, rem = items % slots;
+    time = full * t_item;
+    if (rem) {
+        const long long per_cu = (rem + cus - 1) / cus;
+        double last =
+            per_cu < occ ? t_item * pow((double)per_cu / occ, PARTIAL_EXP) : t_item;
+        if (full == 0 && rem < cus) last *= pow((double)rem / cus, FILL_EXP);
+        time += last;
+    }
+    if (splits > 1) time += (splits + 2.0) * M * N * 4.0 / PARTIALS_BYTES_PER_S + LAUNCH_S;
+    out = Part{t, splits, kchunk};
+    return true;
+}
+
+// The fastest single-band plan of an M x N x K band (split K ranges of at
+// least min_split_k).
+double best_part(const Device &dv, int M, int N, int K, bool may_split, long long max_floats,
+                 Part &best, int min_split_k = 0) {
     double best_t = -1.0;
-    for (int t = 0; t < N_CANDS; ++t) {
-        const B3Cand &c = CANDS[t];
-        const long long tiles = (long long)bmb::ceil_div(M, c.bm) * bmb::ceil_div(N, c.bn);
+    best = Part{0, 1, K};
+    for (int t = 0; t < N_CANDS; ++t)
         for (int s : SPLITS) {
-            int splits = 1, kchunk = K;
-            if (s > 1) {
-                if (!may_split || K < 2 * MIN_SPLIT_K) continue;
-                kchunk = (K + s - 1) / s;
-                kchunk = (kchunk + BK - 1) / BK * BK;
-                if (kchunk < MIN_SPLIT_K) continue;
-                splits = (K + kchunk - 1) / kchunk;
-                if (splits < 2 || (long long)splits * M * N > max_floats) continue;
-                if ((s & (s - 1)) != 0 && kchunk < MIN_ODD_SPLIT_K) continue;
+            Part p;
+            double tm;
+            if (part_time(dv, M, N, K, t, s, may_split, max_floats, p, tm) &&
+                (p.splits == 1 || p.kchunk >= min_split_k) && (best_t < 0 || tm < best_t)) {
+                best_t = tm;
+                best = p;
             }
-            const long long items = tiles * splits;
-            const long long slots = (long long)cus[dev] * occ[dev][t];
-            const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) * occ[dev][t] /
-                                  (c.tflops * 1e12 / cus[dev]);
-            const long long full = items / slots, rem = items % slots;
-            double time = full * t_item;
-            if (rem) {
-                const long long per_cu = (rem + cus[dev] - 1) / cus[dev];
-                double last = per_cu < occ[dev][t]
-                                  ? t_item * pow((double)per_cu / occ[dev][t], PARTIAL_EXP)
-                                  : t_item;
-                if (full == 0 && rem < cus[dev]) last *= pow((double)rem / cus[dev], FILL_EXP);
-                time += last;
-            }
-            if (splits > 1)
-                time += (splits + 2.0) * M * N * 4.0 / PARTIALS_BYTES_PER_S + LAUNCH_S;
-            if (best_t < 0 || time < best_t) {
-                best_t = time;
-                best = Plan{t, splits, kchunk};
+        }
+    return best_t;
+}
+
+Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats) {
+    const Device &dv = device_info(dev);
+    Plan best{{Part{0, 1, K}, Part{0, 1, K}}, M};
+    const double single_t = best_part(dv, M, N, K, may_split, max_floats, best.part[0]);
+    double best_t = single_t;
+    // Two bands: the first whole rounds of one tile, the rest on its own plan.
+    for (int t = 0; K >= MIN_BAND_K && t < N_CANDS; ++t) {
+        const B3Cand &c = CANDS[t];
+        const long long tiles_n = bmb::ceil_div(N, c.bn);
+        const long long slots = (long long)dv.cus * dv.occ[t];
+        for (long long k = 1;; ++k) {
+            const long long rows = k * slots / tiles_n;  // tile rows in k whole rounds
+            if (rows <= 0) continue;
+            if (rows * c.bm >= M) break;
+            const int m1 = (int)(rows * c.bm);
+            Part p0, p1;
+            double t0, t1;
+            if (!part_time(dv, m1, N, K, t, 1, false, 0, p0, t0)) continue;
+            t1 = best_part(dv, M - m1, N, K, may_split, max_floats, p1, MIN_BAND_SPLIT_K);
+            if (t1 < 0) continue;
+            const double tm = t0 + t1 + BAND_S;
+            if (tm < BAND_GAIN * single_t && tm < best_t) {
+                best_t = tm;
+                best = Plan{{p0, p1}, m1};
             }
         }
     }
     return best;
 }
 
+// Plans are memoised per (device, shape, split permission and cap): the
+// search above costs tens of microseconds, a GEMM call in a training step
+// a few hundred.
+Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    using Key = std::tuple<int, int, int, int, bool, long long>;
+    static std::mutex mu;
+    static std::map<Key, Plan> memo;
+    const Key key{dev, M, N, K, may_split, max_floats};
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = memo.find(key);
+        if (it != memo.end()) return it->second;
+    }
+    const Plan p = plan_for(dev, M, N, K, may_split, max_floats);
+    std::lock_guard<std::mutex> lock(mu);
+    if (memo.size() > 4096) memo.clear();
+    memo.emplace(key, p);
+    return p;
+}
+
 template <class Tl, bool TA, bool TB, int EPI>
-void launch(int M, int N, int K, int kchunk, int splits, float alpha, const float *A,
+void launch(int M, int N, int K, int kchunk, int splits, float alpha, const float *A, int lda,
             const float *B, float beta, float *C, bool vec, hipStream_t stream,
             bmb::EpiArgs ep) {
     const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
@@ -697,39 +799,69 @@ void launch(int M, int N, int K, int kchunk, int splits, float alpha, const floa
         auto kern = bf16x3_k<Tl, TA, TB, true, EPI>;
         bmb::allow_smem(kern, Tl::SMEM_BYTES);
         bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    B, beta, C, tiles_m, tiles_n, ep);
+                    lda, B, beta, C, tiles_m, tiles_n, ep);
     } else {
         auto kern = bf16x3_k<Tl, TA, TB, false, EPI>;
         bmb::allow_smem(kern, Tl::SMEM_BYTES);
         bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    B, beta, C, tiles_m, tiles_n, ep);
+                    lda, B, beta, C, tiles_m, tiles_n, ep);
     }
 }
 
-// A plan on tile Tl: one launch with the epilogue, or the split partials
+// One band on tile Tl: one launch with the epilogue, or the split partials
 // (EPI_PARTIAL into P) and the shared reduce with the epilogue.
 template <class Tl, bool TA, bool TB, int EPI>
-void run_plan(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
-              float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
+void run_part(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
+              const float *B, float beta, float *C, bool vec, float *P, hipStream_t stream,
+              bmb::EpiArgs ep) {
     if (p.splits > 1) {
-        launch<Tl, TA, TB, bmb::EPI_PARTIAL>(M, N, K, p.kchunk, p.splits, 1.0f, A, B, 0.0f, P, vec,
-                                             stream, ep);
+        launch<Tl, TA, TB, bmb::EPI_PARTIAL>(M, N, K, p.kchunk, p.splits, 1.0f, A, lda, B, 0.0f,
+                                             P, vec, stream, ep);
         bmb::splitk_reduce_epi(EPI, C, P, p.splits, (long long)M * N, N, alpha, beta, stream,
                                ep.bias, ep.act, ep.pre);
     } else {
-        launch<Tl, TA, TB, EPI>(M, N, K, K, 1, alpha, A, B, beta, C, vec, stream, ep);
+        launch<Tl, TA, TB, EPI>(M, N, K, K, 1, alpha, A, lda, B, beta, C, vec, stream, ep);
     }
 }
 
 template <bool TA, bool TB, int EPI>
-void run_tiles(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
-               float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
+void run_band(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
+              const float *B, float beta, float *C, bool vec, float *P, hipStream_t stream,
+              bmb::EpiArgs ep) {
     switch (p.tile) {
-    case 0: run_plan<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
-    case 1: run_plan<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
-    case 2: run_plan<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
-    default: run_plan<TileT, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep); break;
+    case 0: run_part<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
+    case 1: run_part<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
+    case 2: run_part<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
+    default: run_part<TileT, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
     }
+}
+
+// Both bands of a plan, in row order on one stream (the second band's split
+// partials reuse P after the first band's reduce has read it).
+template <bool TA, bool TB, int EPI>
+void run_plan(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
+              float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
+    const int lda = TA ? M : K;
+    run_band<TA, TB, EPI>(p.part[0], p.m1, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep);
+    if (p.m1 >= M) return;
+    const size_t r = (size_t)p.m1;
+    bmb::EpiArgs e1 = ep;
+    if (e1.act) e1.act += r * N;
+    if (e1.pre) e1.pre += r * N;
+    // A band of rows starts r rows (TA: r columns of the stored K x M) in.
+    const float *A1 = TA ? A + r : A + r * K;
+    // 16-byte loads of the band need its first row aligned as well.
+    const bool vec1 = vec && (((uintptr_t)A1 & 15) == 0);
+    run_band<TA, TB, EPI>(p.part[1], M - p.m1, N, K, alpha, A1, lda, B, beta, C + r * N, vec1,
+                          P, stream, e1);
+}
+
+long long partial_floats(const Plan &p, int M, int N) {
+    long long f = 0;
+    if (p.part[0].splits > 1) f = (long long)p.part[0].splits * p.m1 * N;
+    if (p.m1 < M && p.part[1].splits > 1)
+        f = std::max(f, (long long)p.part[1].splits * (M - p.m1) * N);
+    return f;
 }
 
 }  // namespace
@@ -755,13 +887,14 @@ bool bmb::bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const 
     Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
-    if (p.splits > 1 && fixed == nullptr) {
-        lease.emplace(bmb::SCRATCH_GEMM, (size_t)p.splits * M * N * sizeof(float), stream);
+    const long long pf = partial_floats(p, M, N);
+    if (pf > 0 && fixed == nullptr) {
+        lease.emplace(bmb::SCRATCH_GEMM, (size_t)pf * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick(M, N, K, false, 0);  // no scratch: no split
     }
 #define BMB_B3(TA_, TB_, EPI_)                                                              \
-    run_tiles<TA_, TB_, EPI_>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep);        \
+    run_plan<TA_, TB_, EPI_>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep);         \
     return true;
     if (epi == bmb::EPI_BLAS) {
         if (!ta && !tb) { BMB_B3(false, false, bmb::EPI_BLAS) }

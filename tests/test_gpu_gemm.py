@@ -399,3 +399,38 @@ def test_top_of_range_and_infinities(gpu, math):
     assert np.isnan(got[3, :7]).all()
     rest = np.setdiff1d(np.arange(M), [3, 70])
     assert np.isfinite(got[rest]).all()
+
+
+# ---- row bands: a tile count just above whole rounds runs as two launches
+# (rows [0, m1) on whole rounds of one tile, the rest on its own tile and K
+# split; m1 a multiple of 256). 4097^3 takes two bands in both modes' planners
+# when K >= 4096; the transposed-A cases run the second band with A offset by
+# m1 columns and its full row stride.
+
+@pytest.mark.parametrize("math", [0, 1], ids=["bf16x3", "fp32"])
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+def test_row_bands(gpu, trans, math):
+    import torch
+    M = N = K = 4097
+    ta, tb = trans
+    A = O.fill_xorshift(M * K, 0x3131)
+    B = O.fill_xorshift(K * N, 0x4141)
+    C0 = O.fill_xorshift(M * N, 0x5151)
+    with bmb.gemm_math(math):
+        dA, dB, dC = dev(A), dev(B), dev(C0)
+        print("gemm %s %dx%dx%d math %d" % (_tag(trans), M, N, K, math), flush=True)
+        bmb.gemm(ta, tb, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 1.25, dC.data_ptr())
+        sync("gemm bands")
+    got = dC.cpu().numpy().reshape(M, N)
+    # both sides of every 64-row boundary, and the ragged last rows
+    rows = np.unique(np.r_[np.arange(0, M, 64), np.arange(63, M, 64), M - 2, M - 1])
+    Aop = np.ascontiguousarray((A.reshape(K, M).T if ta else A.reshape(M, K))[rows])
+    c0 = C0.reshape(M, N)[rows]
+    ref = O.gemm_f64(False, tb, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+    err, bad = O.normwise(got[rows], ref)
+    assert bad == 0 and err < 1e-4
+    if math == 0:
+        e3, bound = bf16x3_err(got[rows], False, tb, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+        assert e3 < bound, (e3, bound)
+    else:
+        assert err < fp32_order_bound(K), err
