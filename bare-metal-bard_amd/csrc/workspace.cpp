@@ -13,6 +13,7 @@ struct ScratchBuffer {
     // `recorded` is false until the first return.
     hipEvent_t done = nullptr;
     bool recorded = false;
+    hipStream_t last = nullptr;  // the stream `done` was last recorded on
 };
 
 namespace {
@@ -41,16 +42,20 @@ ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes, hipStream_t stream)
     if (bytes == 0) bytes = 256;
     Pool &p = pool(dev, slot);
     {
-        // The smallest idle buffer that fits; else the largest idle one, to
-        // grow; else a new one.
+        // The smallest idle buffer that fits and was last used on this
+        // stream (no wait on another stream's work); else the smallest that
+        // fits; else the largest idle one, to grow; else a new one.
         std::lock_guard<std::mutex> lock(p.mu);
-        int fit = -1, big = -1;
+        int same = -1, fit = -1, big = -1;
         for (int i = 0; i < (int)p.idle.size(); ++i) {
             const size_t c = p.idle[i]->cap;
+            if (c >= bytes && p.idle[i]->last == stream &&
+                (same < 0 || c < p.idle[same]->cap))
+                same = i;
             if (c >= bytes && (fit < 0 || c < p.idle[fit]->cap)) fit = i;
             if (big < 0 || c > p.idle[big]->cap) big = i;
         }
-        const int pick = fit >= 0 ? fit : big;
+        const int pick = same >= 0 ? same : fit >= 0 ? fit : big;
         if (pick >= 0) {
             buf_ = p.idle[pick];
             p.idle.erase(p.idle.begin() + pick);
@@ -96,6 +101,7 @@ ScratchLease::~ScratchLease() {
         // After everything this lease's caller queued on its stream.
         if (hipEventRecord(buf_->done, stream_) == hipSuccess) {
             buf_->recorded = true;
+            buf_->last = stream_;
         } else {
             (void)hipGetLastError();
             // Unordered reuse is not allowed: wait for the stream instead.

@@ -19,9 +19,10 @@
 // (after every kernel the call queued there), and the next lease makes its
 // own stream wait for that event before anything it queues. Two calls on
 // different streams, or on the null stream from several host threads,
-// therefore never touch one buffer at the same time. A buffer that must grow
-// is freed only after its event has completed. Buffers are kept until the
-// process ends.
+// therefore never touch one buffer at the same time. A lease prefers an idle
+// buffer last used on its own stream, so that work on two streams does not
+// wait on each other through the pool. A buffer that must grow is freed only
+// after its event has completed. Buffers are kept until the process ends.
 #pragma once
 
 #include <stddef.h>
