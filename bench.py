@@ -43,6 +43,13 @@ The same JSON line also carries (none of them is `value`):
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--only sgemm|flash] [--flash-sweep] [--quick]
+       python bench.py --summarize-trace DIR [--region NAME]
+
+Every timed region is wrapped in a roctx range "timed:<region>". Under
+`rocprofv3 --kernel-trace --marker-trace --output-format csv -d DIR -- python3
+bench.py ...`, `--summarize-trace DIR` then prints, per region, the kernels
+dispatched inside it (warm-up excluded) with their count, mean and median
+duration: the figures the profiles quote.
 """
 import argparse
 import json
@@ -89,6 +96,10 @@ def parse():
     ap.add_argument("--flash-sweep", action="store_true",
                     help="also time every forward and backward flash config (as the "
                          "reference's tools/test_flash.cu:198-227,279-319 sweep does)")
+    ap.add_argument("--summarize-trace", metavar="DIR", default=None,
+                    help="summarise a rocprofv3 --kernel-trace --marker-trace CSV output "
+                         "directory by timed region (no GPU work)")
+    ap.add_argument("--region", default=None, help="with --summarize-trace: only this region")
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain 256 MiB device-to-device copy 3 times, the "
                          "known-size reference dispatch for rocprofv3 --pmc FETCH_SIZE / "
@@ -99,6 +110,38 @@ def parse():
 T_START = time.perf_counter()
 
 
+class _Roctx:
+    """roctx ranges around the timed regions (named "timed:<region>"), so that a
+    rocprofv3 run with --marker-trace can attribute kernel dispatches to them
+    (--summarize-trace). Calls into rocprofiler-sdk's roctx library, which
+    does nothing unless a profiler is attached; absent library: no ranges."""
+
+    def __init__(self):
+        import ctypes
+        self.lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so"):
+            try:
+                lib = ctypes.CDLL(name)
+                lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+                lib.roctxRangePushA.restype = ctypes.c_int
+                lib.roctxRangePop.restype = ctypes.c_int
+                self.lib = lib
+                break
+            except OSError:
+                continue
+
+    def push(self, name):
+        if self.lib is not None:
+            self.lib.roctxRangePushA(("timed:" + name).encode())
+
+    def pop(self):
+        if self.lib is not None:
+            self.lib.roctxRangePop()
+
+
+ROCTX = _Roctx()
+
+
 def progress(msg):
     """One line on stderr per finished part of the run (the JSON line alone
     goes to stdout)."""
@@ -106,7 +149,7 @@ def progress(msg):
           flush=True)
 
 
-def timed(fn, steps, warmup):
+def timed(fn, steps, warmup, name="per-launch"):
     """Per-launch durations (ms) from HIP events on the null stream."""
     import torch
     for _ in range(warmup):
@@ -114,11 +157,13 @@ def timed(fn, steps, warmup):
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
+    ROCTX.push(name)
     for a, b in ev:
         a.record()
         fn()
         b.record()
     torch.cuda.synchronize()
+    ROCTX.pop()
     return [a.elapsed_time(b) for a, b in ev]
 
 
@@ -145,6 +190,7 @@ def timed_steps(fn, steps, warmup, name=None):
         WARM_STEPS_RUN[name] = n
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ROCTX.push(name or "region")
     t0 = time.perf_counter()
     a.record()
     for _ in range(steps):
@@ -152,6 +198,7 @@ def timed_steps(fn, steps, warmup, name=None):
     b.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
+    ROCTX.pop()
     return a.elapsed_time(b) / steps, wall
 
 
@@ -256,7 +303,7 @@ def sustained_telemetry(fn, seconds=3.5):
     return tel.result()
 
 
-def timed_burst(fn, reps, warmup=2):
+def timed_burst(fn, reps, warmup=2, name="burst"):
     """Average duration (ms) of `reps` back-to-back launches between one pair
     of HIP events: the throughput of a kernel in a stream, as the training
     step runs it. Per-launch event pairs add a gap of tens of microseconds
@@ -274,11 +321,13 @@ def timed_burst(fn, reps, warmup=2):
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ROCTX.push(name)
     a.record()
     for _ in range(reps):
         fn()
     b.record()
     torch.cuda.synchronize()
+    ROCTX.pop()
     return a.elapsed_time(b) / reps
 
 
@@ -287,7 +336,7 @@ def independent_runs(fn, steps, first_ms, runs=3):
     warm-up and synchronised ends (the first is the reported one): the
     per-step ms of each run, their median, and the spread (max - min over
     the median), flagged above 3%."""
-    ms = [first_ms] + [timed_steps(fn, steps, 2)[0] for _ in range(runs - 1)]
+    ms = [first_ms] + [timed_steps(fn, steps, 2, "rerun")[0] for _ in range(runs - 1)]
     s = sorted(ms)
     med = s[len(s) // 2]
     spread = 100.0 * (s[-1] - s[0]) / med
@@ -462,9 +511,65 @@ def gf(flops, ms):
     return round(flops / ms / 1e6, 1)
 
 
+def summarize_trace(d, only=None):
+    """Kernel dispatches inside each "timed:<region>" roctx range of a
+    rocprofv3 CSV output directory (run_kernel_trace.csv and
+    run_marker_api_trace.csv, any prefix): count, mean, median, min and max
+    duration per kernel, and the region's per-step kernel time when its
+    dispatches repeat per step. Markdown on stdout."""
+    import csv
+    import glob
+    import re
+
+    def one(pattern):
+        f = sorted(glob.glob(os.path.join(d, "**", pattern), recursive=True))
+        if not f:
+            sys.exit("bench.py: no %s under %s" % (pattern, d))
+        return list(csv.DictReader(open(f[0])))
+
+    kernels = one("*kernel_trace.csv")
+    regions = [(m["Function"][len("timed:"):], int(m["Start_Timestamp"]), int(m["End_Timestamp"]))
+               for m in one("*marker_api_trace.csv") if m["Function"].startswith("timed:")]
+
+    def short(name):
+        name = re.sub(r"\(anonymous namespace\)::", "", name)
+        name = re.sub(r"^void ", "", name)
+        depth, out = 0, []
+        for ch in name:  # drop the parameter list, keep template arguments
+            if ch == "(" and depth == 0:
+                break
+            depth += ch == "<"
+            depth -= ch == ">"
+            out.append(ch)
+        return "".join(out)
+
+    seen = {}
+    for rname, t0, t1 in regions:
+        if only and rname != only:
+            continue
+        seen[rname] = seen.get(rname, 0) + 1
+        rows = {}
+        for k in kernels:
+            s, e = int(k["Start_Timestamp"]), int(k["End_Timestamp"])
+            if s >= t0 and e <= t1:
+                rows.setdefault(short(k["Kernel_Name"]), []).append((e - s) / 1e3)
+        print("### region `%s` (occurrence %d): %.3f ms between the range's ends\n"
+              % (rname, seen[rname], (t1 - t0) / 1e6))
+        print("| kernel | calls | mean us | median us | min us | max us | total ms |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for name, v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+            v = sorted(v)
+            print("| `%s` | %d | %.1f | %.1f | %.1f | %.1f | %.3f |"
+                  % (name, len(v), sum(v) / len(v), v[len(v) // 2], v[0], v[-1], sum(v) / 1e3))
+        print()
+
+
 def main():
     global SKIP_TELEMETRY
     args = parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.region)
+        return
     SKIP_TELEMETRY = args.no_telemetry
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU tier); "
@@ -792,6 +897,8 @@ def gpt_step_bench(args, bmb, torch, V, steps=None, warm=None, tag=None):
     for step in range(1, total + 1):
         x, y = batches[step - 1]
         torch.cuda.synchronize()
+        if step == warm + 1:
+            ROCTX.push("gpt" if tag is None else "gpt-" + tag.replace(" ", "-"))
         t0 = time.perf_counter()
         loss = m.forward(x, y)
         m.backward()
@@ -803,6 +910,7 @@ def gpt_step_bench(args, bmb, torch, V, steps=None, warm=None, tag=None):
         times.append((time.perf_counter() - t0) * 1e3)
         losses.append(loss)
         norms.append(gn)
+    ROCTX.pop()
     bmb.check("gpt step")
     progress("config 5 (%s) timed: %.2f ms/step" % (tag or "bf16x3 GEMM",
                                                     sum(times[warm:]) / max(1, steps)))
@@ -915,8 +1023,8 @@ def flash_bench(args, bmb, O, torch, traffic, V):
     verify_flash(V, O, qkv, dout, out, lse, dqkv, dsum, Bf, T, C, NH)
     progress("flash verified")
     tot, wall = timed_steps(step, args.steps, args.warmup, "flash")  # one step = fwd + bwd
-    f_ms, _ = timed_steps(fwd, args.steps, 2)
-    b_ms, _ = timed_steps(bwd, args.steps, 2)
+    f_ms, _ = timed_steps(fwd, args.steps, 2, "flash-fwd")
+    b_ms, _ = timed_steps(bwd, args.steps, 2, "flash-bwd")
     fs, bs = stats(timed(fwd, args.steps, 2)), stats(timed(bwd, args.steps, 2))
     runs = independent_runs(step, args.steps, tot)
     bmb.check("flash")
