@@ -140,6 +140,10 @@ __device__ __forceinline__ float4 load_chunk(const float *P, int rows, int cols,
     return v;
 }
 
+// Epilogues whose edge tiles are shifted back inside C (see MfmaGemm::run).
+template <int EPI>
+constexpr bool SHIFT = EPI == EPI_BLAS || EPI == EPI_PARTIAL;
+
 template <bool TA, bool TB, class Tile, bool VEC>
 struct MfmaGemm {
     using L = MfmaLayout<TA, TB, Tile>;
@@ -338,7 +342,7 @@ struct MfmaGemm {
                                                     float alpha, const float *__restrict__ A,
                                                     const float *__restrict__ B, float beta,
                                                     float *C, int m0, int n0, float *smem,
-                                                    EpiArgs ep) {
+                                                    EpiArgs ep, int mlo, int nlo) {
         constexpr int G = BK / 8;  // 8-k groups per tile (even)
         constexpr bool INTERIOR = MODE != 0;             // no M / N bounds checks
         constexpr bool HINTED = MODE == 1 && HINTS;      // branch-free loop: scheduling hints
@@ -406,13 +410,27 @@ struct MfmaGemm {
             }
         }
 
-        // Epilogue: lanes 0-31 of a register cover 32 consecutive columns, so
-        // each C row segment is one 128-byte coalesced access. What an
-        // epilogue reads (C when beta != 0, the GELU input) is gathered for a
-        // row of FN blocks before any of their results is stored, so 16 * FN
-        // loads per lane are in flight at once; read-use-store per element
-        // would cost one memory round trip per output. Same arithmetic as
-        // store_out.
+        if (INTERIOR && SHIFT<EPI> && (mlo > m0 || nlo > n0))
+            epilogue<EPI, INTERIOR, SHIFT<EPI>>(M, N, alpha, beta, C, m0, n0, ep, mlo, nlo, wm, wn,
+                                                lane, acc);
+        else
+            epilogue<EPI, INTERIOR, false>(M, N, alpha, beta, C, m0, n0, ep, mlo, nlo, wm, wn,
+                                           lane, acc);
+    }
+
+    // Epilogue: lanes 0-31 of a register cover 32 consecutive columns, so
+    // each C row segment is one 128-byte coalesced access. What an epilogue
+    // reads (C when beta != 0, the GELU input) is gathered for a row of FN
+    // blocks before any of their results is stored, so 16 * FN loads per lane
+    // are in flight at once; read-use-store per element would cost one memory
+    // round trip per output. Same arithmetic as store_out. WIN: a shifted edge
+    // tile, storing only rows >= mlo and columns >= nlo (it may read the
+    // others: they are inside C).
+    template <int EPI, bool INTERIOR, bool WIN>
+    __device__ static __forceinline__ void epilogue(int M, int N, float alpha, float beta,
+                                                    float *C, int m0, int n0, EpiArgs ep,
+                                                    int mlo, int nlo, int wm, int wn, int lane,
+                                                    const f32x16 (&acc)[FM][FN]) {
         const int l32 = lane & 31, half = lane >> 5;
         const bool reads = EPI == EPI_GELU_GRAD || (EPI == EPI_BLAS && beta != 0.0f);
         const float *src = EPI == EPI_GELU_GRAD ? ep.pre : C;
@@ -435,11 +453,13 @@ struct MfmaGemm {
             for (int fn = 0; fn < FN; ++fn) {
                 const int col = n0 + wn + fn * 32 + l32;
                 if (!INTERIOR && col >= N) continue;
+                if (WIN && col < nlo) continue;
                 const float bias = (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) ? ep.bias[col] : 0.0f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (!INTERIOR && row >= M) continue;
+                    if (WIN && row < mlo) continue;
                     const size_t idx = (size_t)row * N + col;
                     const float a = acc[fi][fn][r];
                     float v;
@@ -468,13 +488,20 @@ struct MfmaGemm {
                                                const float *__restrict__ B, float beta,
                                                float *C, int m0, int n0, float *smem,
                                                EpiArgs ep = {}) {
-        if (m0 + BM <= M && n0 + BN <= N && K > 0) {
+        // A partial tile at the bottom or right edge of a C at least one tile
+        // large is shifted back to end at the edge, overlapping its
+        // neighbour: it then runs the interior path and stores only the rows
+        // and columns it owns (from m0, n0 on). (BLAS and split-K epilogues
+        // only: the fused ones, used at the GPT's whole-tile shapes, would
+        // spill registers for the second epilogue.)
+        if (SHIFT<EPI> ? (M >= BM && N >= BN && K > 0) : (m0 + BM <= M && n0 + BN <= N && K > 0)) {
+            const int ms = min(m0, M - BM), ns = min(n0, N - BN);
             if (K % BK == 0)
-                run_tile<EPI, 1>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+                run_tile<EPI, 1>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0, n0);
             else
-                run_tile<EPI, 2>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+                run_tile<EPI, 2>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0, n0);
         } else {
-            run_tile<EPI, 0>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep);
+            run_tile<EPI, 0>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep, m0, n0);
         }
     }
 };
