@@ -331,12 +331,12 @@ def timed_burst(fn, reps, warmup=2, name="burst"):
     return a.elapsed_time(b) / reps
 
 
-def independent_runs(fn, steps, first_ms, runs=3):
+def independent_runs(fn, steps, first_ms, runs=3, name="region"):
     """The timed region measured `runs` times in all, each with its own
     warm-up and synchronised ends (the first is the reported one): the
     per-step ms of each run, their median, and the spread (max - min over
     the median), flagged above 3%."""
-    ms = [first_ms] + [timed_steps(fn, steps, 2, "rerun")[0] for _ in range(runs - 1)]
+    ms = [first_ms] + [timed_steps(fn, steps, 2, name + " rerun")[0] for _ in range(runs - 1)]
     s = sorted(ms)
     med = s[len(s) // 2]
     spread = 100.0 * (s[-1] - s[0]) / med
@@ -644,7 +644,7 @@ def main():
         flops = 2.0 * N ** 3
         verify_sq(args.kernel, N)
         ms, wall = timed_steps(sq(args.kernel, N), args.steps, args.warmup, "sgemm")
-        st = stats(timed(sq(args.kernel, N), args.steps, 2))  # per-launch spread
+        st = stats(timed(sq(args.kernel, N), args.steps, 2, "sgemm per-launch"))  # spread
         bmb.check("sgemm")
         g = flops / ms / 1e6
         ent = bmb.find_kernel(args.kernel)
@@ -663,7 +663,8 @@ def main():
                          "peak_is": own_peak(args.kernel)[1],
                          "traffic": traffic.get("sgemm_id%d_%d" % (args.kernel, N))},
             "sgemm_launch_ms": {k: round(v, 4) for k, v in st.items()},
-            "independent_runs": independent_runs(sq(args.kernel, N), args.steps, ms),
+            "independent_runs": independent_runs(sq(args.kernel, N), args.steps, ms,
+                                                 name="sgemm"),
             "warmup_steps_run": WARM_STEPS_RUN.get("sgemm"),
             "vendor_fp32_gemm_gflops": vendor_sq(torch, dA, dB, dC, N) if extras else None,
             "device_telemetry_sustained": sustained_telemetry(sq(args.kernel, N)),
@@ -675,7 +676,7 @@ def main():
             c1 = {}
             for kid in (8, 9, 10):
                 verify_sq(kid, 1024, 1.0, 0.0)
-                ms1 = timed_burst(sq(kid, 1024, 1.0, 0.0), 20, 5)
+                ms1 = timed_burst(sq(kid, 1024, 1.0, 0.0), 20, 5, name="config1 id%d" % kid)
                 c1["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = gf(2.0 * 1024 ** 3, ms1)
             line["config1_n1024_gflops"] = c1
             line["id10_denominator"] = {
@@ -689,7 +690,8 @@ def main():
                 for n in SWEEP_N:
                     verify_sq(kid, n, extra=2)
                     reps = 10 if n <= 4096 else 5
-                    row[str(n)] = gf(2.0 * n ** 3, timed_burst(sq(kid, n), reps))
+                    row[str(n)] = gf(2.0 * n ** 3, timed_burst(
+                        sq(kid, n), reps, name="config2 id%d N=%d" % (kid, n)))
                 sweep["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = row
                 progress("config 2 sweep of id %d timed" % kid)
             bmb.check("sgemm sweep")
@@ -700,7 +702,7 @@ def main():
                 if kid not in (8, 9, 10):  # (verified in the sweep at this size)
                     verify_sq(kid, N, extra=2)
                 reps, warm = (2, 1) if kid <= 2 else (5, 2)
-                s3 = stats(timed(sq(kid, N), reps, warm))
+                s3 = stats(timed(sq(kid, N), reps, warm, "ladder id%d" % kid))
                 pk, pk_name = own_peak(kid)
                 ladder["id%d %s" % (kid, bmb.find_kernel(kid)["name"])] = {
                     "gflops": gf(flops, s3["median_ms"]),
@@ -759,7 +761,8 @@ def sizes_bench(bmb, O, torch):
         for kid in (8, 9, 10):
             fn = sgemm_fn(bmb, kid)
             run = lambda: fn(n, n, n, 1.0, dA.data_ptr(), dB.data_ptr(), 0.5, dC.data_ptr())
-            res["id%d N=%d" % (kid, n)] = gf(2.0 * n ** 3, timed_burst(run, 10 if n > 1024 else 50))
+            res["id%d N=%d" % (kid, n)] = gf(2.0 * n ** 3, timed_burst(
+                run, 10 if n > 1024 else 50, name="sizes id%d N=%d" % (kid, n)))
         bmb.check("sgemm sizes")
         del dA, dB, dC
     return res
@@ -774,8 +777,8 @@ def vendor_sq(torch, dA, dB, dC, N):
     B = dB[:N * N].view(N, N)
     Cm = dC[:N * N].view(N, N)
     fn = lambda: Cm.addmm_(A, B, beta=0.5)
-    timed_steps(fn, 5, 5)
-    return gf(2.0 * N ** 3, timed_burst(fn, 20))
+    timed_steps(fn, 5, 5, "vendor warm-up")
+    return gf(2.0 * N ** 3, timed_burst(fn, 20, name="vendor sgemm"))
 
 
 def gpt_shapes(bmb, O, torch, V):
@@ -838,18 +841,21 @@ def gpt_shapes(bmb, O, torch, V):
                 V.gemm_rows(tag + " dW_TN_beta1", DW.view(cout, cin)[rows_co].cpu().numpy(),
                             np.ascontiguousarray(hDYm[:, rows_co].T), hX, False, cin, BT, 1.0,
                             1.0, hDW0.reshape(cout, cin)[rows_co], mname, 1e-4)
-                g = {"fwd_NT": gf(fl, timed_burst(fwd, reps)),
-                     "dX_NN": gf(fl, timed_burst(dxf, reps)),
-                     "dW_TN_beta1": gf(fl, timed_burst(dwf, reps))}
+                g = {"fwd_NT": gf(fl, timed_burst(fwd, reps, name=tag + " fwd_NT")),
+                     "dX_NN": gf(fl, timed_burst(dxf, reps, name=tag + " dX_NN")),
+                     "dW_TN_beta1": gf(fl, timed_burst(dwf, reps, name=tag + " dW_TN"))}
                 bmb.check("gemm " + name)
             g["pct_of_own_ceiling"] = {k: round(v / 1e3 / ceil * 100, 1) for k, v in g.items()}
             entry[mname] = g
         Xm, Wm = X.view(BT, cin), W.view(cout, cin)
         Ym, DYm, DXm = Y.view(BT, cout), DY.view(BT, cout), DX.view(BT, cin)
         entry["vendor_fp32"] = {
-            "fwd_NT": gf(fl, timed_burst(lambda: torch.matmul(Xm, Wm.t(), out=Ym), reps)),
-            "dX_NN": gf(fl, timed_burst(lambda: torch.matmul(DYm, Wm, out=DXm), reps)),
-            "dW_TN_beta1": gf(fl, timed_burst(lambda: Wm.addmm_(DYm.t(), Xm), reps))}
+            "fwd_NT": gf(fl, timed_burst(lambda: torch.matmul(Xm, Wm.t(), out=Ym), reps,
+                                         name="config3 %s vendor fwd_NT" % name)),
+            "dX_NN": gf(fl, timed_burst(lambda: torch.matmul(DYm, Wm, out=DXm), reps,
+                                        name="config3 %s vendor dX_NN" % name)),
+            "dW_TN_beta1": gf(fl, timed_burst(lambda: Wm.addmm_(DYm.t(), Xm), reps,
+                                              name="config3 %s vendor dW_TN" % name))}
         res[name] = entry
         progress("config 3 %s verified and timed" % name)
         del X, W, DY, Y, DX, DW, Xm, Wm, Ym, DYm, DXm
@@ -1025,8 +1031,9 @@ def flash_bench(args, bmb, O, torch, traffic, V):
     tot, wall = timed_steps(step, args.steps, args.warmup, "flash")  # one step = fwd + bwd
     f_ms, _ = timed_steps(fwd, args.steps, 2, "flash-fwd")
     b_ms, _ = timed_steps(bwd, args.steps, 2, "flash-bwd")
-    fs, bs = stats(timed(fwd, args.steps, 2)), stats(timed(bwd, args.steps, 2))
-    runs = independent_runs(step, args.steps, tot)
+    fs = stats(timed(fwd, args.steps, 2, "flash-fwd per-launch"))
+    bs = stats(timed(bwd, args.steps, 2, "flash-bwd per-launch"))
+    runs = independent_runs(step, args.steps, tot, name="flash")
     bmb.check("flash")
     pairs = Bf * NH * T * (T + 1) / 2
     fwd_fl, bwd_fl = 4.0 * hs * pairs, 10.0 * hs * pairs
@@ -1064,14 +1071,14 @@ def flash_bench(args, bmb, O, torch, traffic, V):
         for i, name in enumerate(bmb.flash_configs()):
             f = lambda i=i: bmb.flash_forward_cfg(i, out.data_ptr(), lse.data_ptr(),
                                                   d_qkv.data_ptr(), Bf, T, C, NH)
-            ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+            ms_ = stats(timed(f, max(3, args.steps // 2), 2, "flash fwd cfg %d" % i))["median_ms"]
             sweep["fwd %d %s" % (i, name)] = round(fwd_fl / ms_ / 1e9, 2)
         fwd()
         for i, name in enumerate(bmb.flash_bwd_configs()):
             f = lambda i=i: bmb.flash_backward_cfg(
                 i, dqkv.data_ptr(), dsum.data_ptr(), d_dout.data_ptr(), d_qkv.data_ptr(),
                 out.data_ptr(), lse.data_ptr(), Bf, T, C, NH)
-            ms_ = stats(timed(f, max(3, args.steps // 2), 2))["median_ms"]
+            ms_ = stats(timed(f, max(3, args.steps // 2), 2, "flash bwd cfg %d" % i))["median_ms"]
             sweep["bwd %d %s" % (i, name)] = round(bwd_fl / ms_ / 1e9, 2)
         bmb.check("flash sweep")
         flash["config_sweep_tflops"] = sweep
