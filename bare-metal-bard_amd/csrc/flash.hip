@@ -56,6 +56,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <functional>
 #include <map>
 #include <mutex>
@@ -2197,18 +2198,21 @@ flash_bwd_h_k(float *__restrict__ dqkv, const float *__restrict__ qkv,
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Per device, read once; concurrent first calls store the same value.
 int cus_per_xcd() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
-    if (cached[dev] == 0) {
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                 hipSuccess || cus < NXCD)
             cus = 256;
-        cached[dev] = cus / NXCD;
+        v = cus / NXCD;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return v;
 }
 
 // Forward tile configs. wpb: 32-query waves per workgroup (they share every

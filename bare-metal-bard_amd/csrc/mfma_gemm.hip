@@ -64,16 +64,29 @@ int device_cus() {
 // costs the partials' round trip (mostly through the 256 MB last-level
 // cache, hence a rate above HBM's) plus one reduce launch. The model only
 // compares candidates; its times are not predictions.
+//
+// A candidate with ks > 1 runs each output tile as ks k-slices of one
+// workgroup (ks times the waves; the slices' sums meet in LDS, with no
+// partials in global memory and no reduce launch): for few output tiles it
+// puts more waves on each SIMD without split-K's round trip. Those kernels
+// exist for the plain BLAS epilogue only (KERNELS id 9, gemm() in fp32 mode,
+// batched_gemm()).
 enum class TileKind { L, M, N, S };
 struct Cand {
     TileKind kind;
     int bm, bn;
     double eff;
+    int ks;
 };
-constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.909},
-                          {TileKind::M, 128, 128, 0.893},
-                          {TileKind::N, 64, 128, 0.823},
-                          {TileKind::S, 64, 64, 0.809}};
+constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.909, 1},
+                          {TileKind::M, 128, 128, 0.893, 1},
+                          {TileKind::N, 64, 128, 0.823, 1},
+                          {TileKind::S, 64, 64, 0.809, 1},
+                          {TileKind::M, 128, 128, 0.893, 2},
+                          {TileKind::N, 64, 128, 0.823, 2},
+                          {TileKind::N, 64, 128, 0.823, 4},
+                          {TileKind::S, 64, 64, 0.809, 2},
+                          {TileKind::S, 64, 64, 0.809, 4}};
 constexpr int N_CANDS = sizeof(CANDS) / sizeof(CANDS[0]);
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 constexpr double K_OVERHEAD = 60.0;           // per-item prologue/epilogue, in k steps
@@ -81,6 +94,7 @@ constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last rou
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
 constexpr int MIN_SPLIT_K = 128;              // shortest K range a split may get
+constexpr int MIN_SLICE_K = 64;               // shortest K range a k-slice may get
 // A second band: its launch and the drain between the bands. Bands are only
 // tried for K >= MIN_BAND_K, with K ranges of at least MIN_BAND_SPLIT_K in a
 // split remainder band, and taken when modelled 3% faster than one band (as
@@ -156,10 +170,22 @@ void tile_occupancy(int (&out)[2]) {
     out[1] = wgs_per_cu(bmb::mfma_gemm_splitk_k<TA, TB, Tile, VEC>, Tile::NT, L::SMEM_BYTES);
 }
 
+// The k-sliced kernel's workgroups per CU ([1]: unused, it never splits K
+// across workgroups); 0 when the case has no k-sliced kernel.
+template <bool TA, bool TB, class Tile, int EPI, bool VEC, int KS>
+void ks_occupancy(int (&out)[2]) {
+    using L = bmb::MfmaLayout<TA, TB, Tile>;
+    out[0] = EPI == bmb::EPI_BLAS
+                 ? wgs_per_cu(bmb::mfma_gemm_ks_k<TA, TB, Tile, VEC, bmb::EPI_BLAS, KS>,
+                              Tile::NT * KS, KS * L::SMEM_BYTES)
+                 : 0;
+    out[1] = 0;
+}
+
 // One band's launch: tile candidate, K ranges (1: no split) and the K per
 // range (a multiple of 16).
 struct Part {
-    int tile;
+    int tile;  // index into CANDS (its ks: k-slices per workgroup)
     int splits;
     int kchunk;
 };
@@ -184,6 +210,7 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     const long long slots = (long long)cus * occ;
     const double peak_cu = 157.3e12 / 256.0;
     const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) / (c.eff * peak_cu) * occ;
+    // (a k-sliced workgroup: occ counts workgroups of ks slices each)
     const long long full = items / slots, rem = items % slots;
     double t = full * t_item;
     if (rem) {
@@ -205,10 +232,12 @@ double best_part(int M, int N, int K, int batch, bool may_split, const Occupancy
     double best_t = -1.0;
     for (int ci = 0; ci < N_CANDS; ++ci) {
         const Cand &c = CANDS[ci];
+        if (occ.wgs[ci][0] <= 0) continue;  // no such kernel for this case
+        if (c.ks > 1 && K < c.ks * MIN_SLICE_K) continue;
         for (int s : SPLITS) {
             int splits = 1, kchunk = round_up16(K);
             if (s > 1) {
-                if (!may_split || K < 2 * MIN_SPLIT_K) continue;
+                if (c.ks > 1 || !may_split || K < 2 * MIN_SPLIT_K) continue;
                 kchunk = round_up32((K + s - 1) / s);  // whole k-tiles of every tile's BK
                 if (kchunk < MIN_SPLIT_K) continue;
                 splits = (K + kchunk - 1) / kchunk;
@@ -236,6 +265,7 @@ Plan plan_for(int M, int N, int K, int batch, bool may_split, const Occupancy &o
     double best_t = single_t;
     for (int ci = 0; ci < N_CANDS; ++ci) {
         const Cand &c = CANDS[ci];
+        if (c.ks > 1) continue;  // a first band of whole rounds: plain tiles
         const long long tiles_n = (N + c.bn - 1) / c.bn;
         const long long slots = (long long)cus * occ.wgs[ci][0];
         for (long long k = 1;; ++k) {
@@ -295,11 +325,21 @@ const Occupancy &occupancy(bool vec) {
             tile_occupancy<TA, TB, TileM, EPI, true>(o.wgs[1]);
             tile_occupancy<TA, TB, TileN, EPI, true>(o.wgs[2]);
             tile_occupancy<TA, TB, TileS, EPI, true>(o.wgs[3]);
+            ks_occupancy<TA, TB, TileM, EPI, true, 2>(o.wgs[4]);
+            ks_occupancy<TA, TB, TileN, EPI, true, 2>(o.wgs[5]);
+            ks_occupancy<TA, TB, TileN, EPI, true, 4>(o.wgs[6]);
+            ks_occupancy<TA, TB, TileS, EPI, true, 2>(o.wgs[7]);
+            ks_occupancy<TA, TB, TileS, EPI, true, 4>(o.wgs[8]);
         } else {
             tile_occupancy<TA, TB, TileL, EPI, false>(o.wgs[0]);
             tile_occupancy<TA, TB, TileM, EPI, false>(o.wgs[1]);
             tile_occupancy<TA, TB, TileN, EPI, false>(o.wgs[2]);
             tile_occupancy<TA, TB, TileS, EPI, false>(o.wgs[3]);
+            ks_occupancy<TA, TB, TileM, EPI, false, 2>(o.wgs[4]);
+            ks_occupancy<TA, TB, TileN, EPI, false, 2>(o.wgs[5]);
+            ks_occupancy<TA, TB, TileN, EPI, false, 4>(o.wgs[6]);
+            ks_occupancy<TA, TB, TileS, EPI, false, 2>(o.wgs[7]);
+            ks_occupancy<TA, TB, TileS, EPI, false, 4>(o.wgs[8]);
         }
     });
     return table[dev][vec];
@@ -322,6 +362,30 @@ void launch_tile(int batch, int M, int N, int K, float alpha, const float *A, in
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, grid, dim3(Tile::NT),
                     L::SMEM_BYTES, stream, M, N, K, alpha, A, lda, sA, B, sB, beta, C,
                     sC, tiles_m, tiles_n, ep);
+    }
+}
+
+// A tile as KS k-slices of one workgroup (EPI_BLAS only).
+template <bool TA, bool TB, class Tile, int EPI, int KS>
+void launch_tile_ks(int batch, int M, int N, int K, float alpha, const float *A, int lda,
+                    long long sA, const float *B, long long sB, float beta, float *C,
+                    long long sC, hipStream_t stream, bool vec) {
+    if constexpr (EPI == bmb::EPI_BLAS) {
+        using L = bmb::MfmaLayout<TA, TB, Tile>;
+        const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
+        const dim3 grid(tiles_m * tiles_n, batch);
+        const size_t smem = KS * L::SMEM_BYTES;
+        if (vec) {
+            auto k = bmb::mfma_gemm_ks_k<TA, TB, Tile, true, EPI, KS>;
+            bmb::allow_smem(k, smem);
+            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, A, lda, sA,
+                        B, sB, beta, C, sC, tiles_m, tiles_n, bmb::EpiArgs{});
+        } else {
+            auto k = bmb::mfma_gemm_ks_k<TA, TB, Tile, false, EPI, KS>;
+            bmb::allow_smem(k, smem);
+            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, A, lda, sA,
+                        B, sB, beta, C, sC, tiles_m, tiles_n, bmb::EpiArgs{});
+        }
     }
 }
 
@@ -358,6 +422,23 @@ void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const 
         case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
         case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
         case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        }
+        return;
+    }
+    if (CANDS[p.tile].ks > 1) {
+        const int ks = CANDS[p.tile].ks;
+        switch (CANDS[p.tile].kind) {
+        case TileKind::M:
+            launch_tile_ks<TA, TB, TileM, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            break;
+        case TileKind::N:
+            if (ks == 2) launch_tile_ks<TA, TB, TileN, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            else launch_tile_ks<TA, TB, TileN, EPI, 4>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            break;
+        default:
+            if (ks == 2) launch_tile_ks<TA, TB, TileS, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            else launch_tile_ks<TA, TB, TileS, EPI, 4>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            break;
         }
         return;
     }

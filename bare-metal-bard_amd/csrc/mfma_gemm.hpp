@@ -334,10 +334,19 @@ struct MfmaGemm {
 
     // One output tile (m0, n0) of one problem over k in [0, K); A and B are
     // positioned at k = 0 of that range, lda / ldb are their row strides.
-    // smem holds two stages. EPI selects what is stored (see Epi). MODE (see
-    // load_tile): 1 and 2 need the tile inside M x N and K > 0, 1 also
-    // K % BK == 0.
-    template <int EPI, int MODE>
+    // smem holds two stages per k-slice. EPI selects what is stored (see
+    // Epi). MODE (see load_tile): 1 and 2 need the tile inside M x N and
+    // K > 0, 1 also K % (BK * KS) == 0.
+    //
+    // KS > 1 (a k-sliced workgroup of KS * NT threads): slice s stages and
+    // multiplies k-tiles [s * per, (s + 1) * per) of the range in its own two
+    // LDS stages, per = ceil(k-tiles / KS). Every slice runs `per` k-tiles, so
+    // all reach the same barriers; a slice's k-tiles past K load zeros. The
+    // slices' sums then meet in LDS and slice 0 adds them in slice order
+    // (deterministic) and runs the epilogue. For tiles too few to give every
+    // SIMD two waves (N <= 1024 or so), this doubles the waves per tile with
+    // no split-K partials in global memory and no reduce launch.
+    template <int EPI, int MODE, int KS = 1>
     __device__ static __forceinline__ void run_tile(int M, int N, int K, int lda, int ldb,
                                                     float alpha, const float *__restrict__ A,
                                                     const float *__restrict__ B, float beta,
@@ -346,10 +355,12 @@ struct MfmaGemm {
         constexpr int G = BK / 8;  // 8-k groups per tile (even)
         constexpr bool INTERIOR = MODE != 0;             // no M / N bounds checks
         constexpr bool HINTED = MODE == 1 && HINTS;      // branch-free loop: scheduling hints
-        const int tid = threadIdx.x;
+        const int slice = KS > 1 ? (int)threadIdx.x / NT : 0;
+        const int tid = KS > 1 ? (int)threadIdx.x % NT : (int)threadIdx.x;
         const int wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tile::WAVES_N) * WM;
         const int wn = (wave % Tile::WAVES_N) * WN;
+        float *const smem0 = smem;
 
         f32x16 acc[FM][FN];
 #pragma unroll
@@ -359,23 +370,39 @@ struct MfmaGemm {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[fi][fn][r] = 0.0f;
 
+        // k-tiles every slice runs (the same in all slices: they share the
+        // barriers), then this slice's own range and k-tiles.
+        int nkt_iter = (K + BK - 1) / BK;
+        if (KS > 1) {
+            const int per = (nkt_iter + KS - 1) / KS;
+            const int kb = min(K, slice * per * BK);
+            const int klen = min(K, kb + per * BK) - kb;
+            A += TA ? (size_t)kb * lda : (size_t)kb;
+            B += TB ? (size_t)kb : (size_t)kb * ldb;
+            K = klen;
+            smem += slice * 2 * L::STAGE;
+            nkt_iter = per;
+        }
         const int nkt = (K + BK - 1) / BK;
-        if (nkt > 0) {
+        if (nkt_iter > 0) {
             Regs g;
             if (INTERIOR) {
                 load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0, 0, nkt, tid);
                 store(g, smem, smem + L::A_SZ, tid);
-                load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0, min(1, nkt - 1), nkt, tid);
+                // (MODE 1: every slice has nkt whole k-tiles, clamp into
+                // them; a k-sliced MODE 2 slice loads zeros past its range.)
+                load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0,
+                                (MODE == 1 || KS == 1) ? min(1, nkt - 1) : 1, nkt, tid);
             } else {
                 load(g, A, B, M, N, K, lda, ldb, m0, n0, 0, tid);
                 store(g, smem, smem + L::A_SZ, tid);
-                if (nkt > 1) load(g, A, B, M, N, K, lda, ldb, m0, n0, BK, tid);
+                if (nkt_iter > 1) load(g, A, B, M, N, K, lda, ldb, m0, n0, BK, tid);
             }
             __syncthreads();
 
             float fa[2][FM][4], fb[2][FN][4];
             fragments(smem, smem + L::A_SZ, 0, wm, wn, lane, fa[0], fb[0]);
-            for (int kt = 0; kt < nkt; ++kt) {
+            for (int kt = 0; kt < nkt_iter; ++kt) {
                 const float *as = smem + (kt & 1) * L::STAGE, *bs = as + L::A_SZ;
 #pragma unroll
                 for (int grp = 0; grp < G; ++grp) {
@@ -393,11 +420,14 @@ struct MfmaGemm {
                         // Guarding them makes the compiler copy the fragment
                         // registers and wait for the reads before this
                         // group's MFMAs.
+                        // (A k-sliced MODE 2 tile loads zeros past its range
+                        // instead: it may run k-tiles beyond it.)
                         float *nxt = smem + ((kt + 1) & 1) * L::STAGE;
                         store(g, nxt, nxt + L::A_SZ, tid);
                         if (INTERIOR)
                             load_tile<MODE>(g, A, B, M, N, K, lda, ldb, m0, n0,
-                                            min(kt + 2, nkt - 1), nkt, tid);
+                                            (MODE == 1 || KS == 1) ? min(kt + 2, nkt - 1) : kt + 2,
+                                            nkt, tid);
                         else
                             load(g, A, B, M, N, K, lda, ldb, m0, n0, (kt + 2) * BK, tid);
                         if (HINTED) hint_before_barrier();
@@ -407,6 +437,40 @@ struct MfmaGemm {
                     mma(fa[cb], fb[cb], acc);
                     if (HINTED && grp == G - 1) hint_after_barrier();
                 }
+            }
+        }
+
+        if (KS > 1) {
+            // Slices 1.. leave their sums in LDS (the staging stages are
+            // idle once every slice is past its last fragment read); slice 0
+            // adds them in slice order. Lane-contiguous: no bank conflicts.
+            static_assert(KS == 1 || (size_t)(KS - 1) * BM * BN <= (size_t)KS * 2 * L::STAGE,
+                          "the slices' sums fit in the staging LDS");
+            constexpr int PER = FM * FN * 16;
+            __syncthreads();
+            if (slice > 0) {
+                float *dst = smem0 + (size_t)(slice - 1) * BM * BN + (size_t)wave * PER * 64 + lane;
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            dst[((fi * FN + fn) * 16 + r) * 64] = acc[fi][fn][r];
+            }
+            __syncthreads();
+            if (slice > 0) return;
+#pragma unroll
+            for (int s = 1; s < KS; ++s) {
+                const float *src =
+                    smem0 + (size_t)(s - 1) * BM * BN + (size_t)wave * PER * 64 + lane;
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[fi][fn][r] += src[((fi * FN + fn) * 16 + r) * 64];
             }
         }
 
@@ -481,8 +545,8 @@ struct MfmaGemm {
 
     // Picks the interior path when it applies (a uniform branch per workgroup),
     // with or without 16-byte aligned operands; a K that is not a whole number
-    // of k-tiles guards only the last k-tile's loads.
-    template <int EPI = EPI_BLAS>
+    // of k-tiles (per slice) guards only the last k-tile's loads.
+    template <int EPI = EPI_BLAS, int KS = 1>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
                                                float alpha, const float *__restrict__ A,
                                                const float *__restrict__ B, float beta,
@@ -496,12 +560,15 @@ struct MfmaGemm {
         // spill registers for the second epilogue.)
         if (SHIFT<EPI> ? (M >= BM && N >= BN && K > 0) : (m0 + BM <= M && n0 + BN <= N && K > 0)) {
             const int ms = min(m0, M - BM), ns = min(n0, N - BN);
-            if (K % BK == 0)
-                run_tile<EPI, 1>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0, n0);
+            if (K % (BK * KS) == 0)
+                run_tile<EPI, 1, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0,
+                                     n0);
             else
-                run_tile<EPI, 2>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0, n0);
+                run_tile<EPI, 2, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0,
+                                     n0);
         } else {
-            run_tile<EPI, 0>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep, m0, n0);
+            run_tile<EPI, 0, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep, m0,
+                                 n0);
         }
     }
 };
@@ -523,6 +590,23 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
     MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, lda, TB ? K : N, alpha,
                                                    A + z * sA, B + z * sB, beta, C + z * sC,
                                                    tm * Tile::BM, tn * Tile::BN, smem_dyn, ep);
+}
+
+// The same with KS k-slices per workgroup (KS * NT threads; LDS: KS times
+// the stages of one).
+template <bool TA, bool TB, class Tile, bool VEC, int EPI, int KS>
+__global__ __launch_bounds__(Tile::NT * KS) void mfma_gemm_ks_k(
+    int M, int N, int K, float alpha, const float *__restrict__ A, int lda,
+    long long sA, const float *__restrict__ B, long long sB, float beta,
+    float *C, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
+    extern __shared__ float smem_dyn[];
+    const size_t z = blockIdx.y;
+    int tm, tn;
+    group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI, KS>(M, N, K, lda, TB ? K : N, alpha,
+                                                       A + z * sA, B + z * sB, beta, C + z * sC,
+                                                       tm * Tile::BM, tn * Tile::BN, smem_dyn,
+                                                       ep);
 }
 
 // Split-K: blockIdx.y = split s covers k in [s*kchunk, min(K, (s+1)*kchunk))

@@ -121,6 +121,39 @@ def test_batched_gemm(gpu, bshape, trans):
     assert bad == 0 and err < 1e-4
 
 
+# Few output tiles and a long K: batched_gemm() never splits K across
+# workgroups, so the planner runs such tiles as k-slices of one workgroup
+# (2 or 4 slices summed in LDS). Whole tiles with K a multiple of the slices'
+# k-tiles, K that leaves the last slice short or empty, tiles shifted back
+# at the edges, and problems smaller than one tile.
+KSHAPES = [(2, 128, 128, 2048), (3, 100, 70, 3000), (2, 40, 50, 1100), (3, 64, 256, 4160),
+           (1, 200, 136, 1000), (2, 64, 64, 72 * 16 + 8)]
+
+
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("bshape", KSHAPES, ids=lambda s: "b%d_%dx%dx%d" % s)
+def test_batched_long_k(gpu, bshape, trans):
+    """Within fp32_order_bound(K) of the fp64 product (fp32 MFMA products;
+    only the summation order differs)."""
+    batch, M, N, K = bshape
+    ta, tb = trans
+    eA, eB, eC = M * K, K * N, M * N
+    A = O.fill_xorshift(eA * batch, 0x2468)
+    B = O.fill_xorshift(eB * batch, 0x1357)
+    C0 = O.fill_xorshift(eC * batch, 0x4444)
+    dA, dB = dev(A), dev(B)
+    gC = Guarded(eC * batch, fill=C0)
+    print("batched long-K %s batch=%d M=%d N=%d K=%d" % (_tag(trans), batch, M, N, K), flush=True)
+    bmb.batched_gemm(ta, tb, batch, M, N, K, 0.5, dA.data_ptr(), eA, dB.data_ptr(), eB,
+                     2.0, gC.ptr, eC)
+    sync("batched_gemm")
+    assert gC.ok()
+    ref = O.batched_gemm_f64(ta, tb, batch, M, N, K, 0.5, A, eA, B, eB, 2.0, C0, eC)
+    err, bad = O.normwise(gC.get(), ref)
+    print("  normwise %.2e (bound %.2e)" % (err, fp32_order_bound(K)))
+    assert bad == 0 and err < fp32_order_bound(K)
+
+
 # BASELINE config 3: the 15 GEMMs of the GPT-2-small step (BT = 8192,
 # C = 768, V = 50257), i.e. every (layer, pass) that bench.py times. Layer
 # (cin, cout): forward y = x w^T is NT (BT, cout, cin); dX = dy w is NN
