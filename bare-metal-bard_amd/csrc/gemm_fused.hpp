@@ -27,9 +27,10 @@ void splitk_reduce(float *C, const float *P, int splits, long long mn, int N, fl
                    float beta, hipStream_t stream);
 
 // The same reduce ending in epilogue `epi` (an Epi of mfma_gemm.hpp: bias[N],
-// act = gelu(C) output, pre = the GELU input, as the GEMM epilogues).
+// act = gelu(C) output, pre = the GELU input, as the GEMM epilogues), C's
+// rows (and those of act, pre) ldc floats apart.
 void splitk_reduce_epi(int epi, float *C, const float *P, int splits, long long mn, int N,
-                       float alpha, float beta, hipStream_t stream, const float *bias,
+                       int ldc, float alpha, float beta, hipStream_t stream, const float *bias,
                        float *act, const float *pre);
 
 // Row-major C[M,N] = epilogue(op(A) @ op(B)) on bf16x3 matrix-core products
@@ -43,5 +44,21 @@ bool bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const float
                  const float *B, float beta, float *C, hipStream_t stream, int epi,
                  const float *bias, float *act, const float *pre, float *fixed,
                  long long fixed_floats);
+
+// Thin edges of a corner plan (edge_gemm.hip): of an M x N x K problem with
+// row-major A (lda), B (ldb) and C (ldc), C = alpha A B + beta C over rows
+// [0, m1) x columns [n1, N) and rows [m1, M) x all columns, where N - n1 and
+// M - m1 are at most EDGE_MAX. bf16x3: products as the bf16x3 kernels form
+// them (hi*hi + hi*lo + lo*hi of their split), else exact fp32 products. P:
+// edge_partial_floats(M - m1, N - n1, N, K) floats of scratch (the bottom
+// edge's partials and a packed copy of B's right edge).
+constexpr int EDGE_MAX = 8;
+int edge_ranges(int N, int K);
+long long edge_partial_floats(int rm, int rn, int N, int K);
+// Modelled time of the edges (seconds), for the planners.
+double edge_model_s(long long m1, long long rn, long long rm, long long N, long long K);
+void gemm_edges(bool bf16x3, int M, int N, int K, int m1, int n1, float alpha, const float *A,
+                int lda, const float *B, int ldb, float beta, float *C, int ldc, float *P,
+                hipStream_t stream);
 
 }  // namespace bmb

@@ -9,6 +9,7 @@
 // the operands is 16-byte aligned.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <atomic>
@@ -190,14 +191,21 @@ struct Part {
     int kchunk;
 };
 
-// Rows [0, m1) run on part[0], rows [m1, M) on part[1] (m1 == M: one band).
-// As in the bf16x3 planner (sgemm_bf16x3.hip), a tile count just above a
-// whole number of rounds (4097^2 on 256 x 256: 289 tiles on 256 CUs) is run
-// as a first band of whole rounds and a remainder band on its own tile and
-// split, one launch after the other on the same stream.
+// Rows [0, m1) x columns [0, n1) run on part[0], rows [0, m1) x columns
+// [n1, N) on part[2], rows [m1, M) x all columns on part[1] (m1 == M: no row
+// band; n1 == N: no column band), one launch after the other on the same
+// stream. As in the bf16x3 planner (sgemm_bf16x3.hip), a tile count just
+// above a whole number of rounds (4097^2 on 256 x 256: 289 tiles on 256 CUs)
+// is run as a first band of whole rounds and a remainder band on its own
+// tile and split. A corner plan instead runs the largest block of whole
+// tiles (4096^2 of 4097^2) on them, and the thin right and bottom edges
+// (4096 x 1 and 1 x 4097) as problems of their own, so no tile computes
+// rows or columns outside C. edges: those edges are at most EDGE_MAX wide
+// and run on the edge kernels (edge_gemm.hip) instead of part[1], part[2].
 struct Plan {
-    Part part[2];
-    int m1;
+    Part part[3];
+    int m1, n1;
+    bool edges;
 };
 
 inline int round_up16(long long x) { return (int)((x + 15) / 16 * 16); }
@@ -256,13 +264,52 @@ double best_part(int M, int N, int K, int batch, bool may_split, const Occupancy
 }
 
 Plan plan_for(int M, int N, int K, int batch, bool may_split, const Occupancy &occ,
-              long long max_floats) {
+              long long max_floats, bool edges_ok) {
     const int cus = device_cus();
-    Plan best{{Part{0, 1, round_up16(K)}, Part{0, 1, round_up16(K)}}, M};
+    const Part whole{0, 1, round_up16(K)};
+    Plan best{{whole, whole, whole}, M, N, false};
     const double single_t = best_part(M, N, K, batch, may_split, occ, max_floats, cus,
                                       best.part[0]);
     if (batch != 1 || K < MIN_BAND_K) return best;
     double best_t = single_t;
+    // Corner plans: whole tiles of one candidate over [0, m1) x [0, n1), the
+    // edges on the best plan of their own.
+    for (int ci = 0; ci < N_CANDS; ++ci) {
+        const Cand &c = CANDS[ci];
+        if (c.ks > 1) continue;
+        const int m1 = M / c.bm * c.bm, n1 = N / c.bn * c.bn;
+        if (m1 == 0 || n1 == 0 || (m1 == M && n1 == N)) continue;
+        double tm = model_time(m1, n1, K, 1, c, occ.wgs[ci][0], 1, round_up16(K), cus);
+        Part pr = whole, pb = whole;
+        if (n1 < N) {
+            const double t = best_part(m1, N - n1, K, 1, may_split, occ, max_floats, cus, pr,
+                                       MIN_BAND_SPLIT_K);
+            if (t < 0) continue;
+            tm += t + BAND_S;
+        }
+        if (m1 < M) {
+            const double t = best_part(M - m1, N, K, 1, may_split, occ, max_floats, cus, pb,
+                                       MIN_BAND_SPLIT_K);
+            if (t < 0) continue;
+            tm += t + BAND_S;
+        }
+        if (tm < BAND_GAIN * single_t && tm < best_t) {
+            best_t = tm;
+            best = Plan{{Part{ci, 1, round_up16(K)}, pb, pr}, m1, n1, false};
+        }
+        // The same block with the edge kernels (row-major A and B, BLAS
+        // epilogue, edges at most EDGE_MAX wide).
+        // (The edges need scratch: only where K may be split.)
+        if (edges_ok && M - m1 <= bmb::EDGE_MAX && N - n1 <= bmb::EDGE_MAX &&
+            may_split && bmb::edge_partial_floats(M - m1, N - n1, N, K) <= max_floats) {
+            const double te = model_time(m1, n1, K, 1, c, occ.wgs[ci][0], 1, round_up16(K), cus) +
+                              bmb::edge_model_s(m1, N - n1, M - m1, N, K);
+            if (te < BAND_GAIN * single_t && te < best_t) {
+                best_t = te;
+                best = Plan{{Part{ci, 1, round_up16(K)}, whole, whole}, m1, n1, true};
+            }
+        }
+    }
     for (int ci = 0; ci < N_CANDS; ++ci) {
         const Cand &c = CANDS[ci];
         if (c.ks > 1) continue;  // a first band of whole rounds: plain tiles
@@ -281,10 +328,17 @@ Plan plan_for(int M, int N, int K, int batch, bool may_split, const Occupancy &o
             const double tm = t0 + t1 + BAND_S;
             if (tm < BAND_GAIN * single_t && tm < best_t) {
                 best_t = tm;
-                best = Plan{{Part{ci, 1, round_up16(K)}, p1}, m1};
+                best = Plan{{Part{ci, 1, round_up16(K)}, p1, whole}, m1, N, false};
             }
         }
     }
+    if (getenv("BMB_GEMM_PLAN_TRACE") != nullptr)
+        fprintf(stderr, "fp32 gemm plan %dx%dx%d: m1 %d n1 %d edges %d parts (%d,%d,%d) "
+                        "(%d,%d,%d) (%d,%d,%d) model %.1f us (one band %.1f us)\n",
+                M, N, K, best.m1, best.n1, (int)best.edges, best.part[0].tile, best.part[0].splits,
+                best.part[0].kchunk, best.part[1].tile, best.part[1].splits, best.part[1].kchunk,
+                best.part[2].tile, best.part[2].splits, best.part[2].kchunk, best_t * 1e6,
+                single_t * 1e6);
     return best;
 }
 
@@ -303,7 +357,8 @@ Plan pick(int M, int N, int K, int batch, bool vec, bool may_split, const Occupa
         auto it = memo.find(key);
         if (it != memo.end()) return it->second;
     }
-    const Plan p = plan_for(M, N, K, batch, may_split, occ, max_floats);
+    const Plan p = plan_for(M, N, K, batch, may_split, occ, max_floats,
+                            !TA && !TB && EPI == bmb::EPI_BLAS);
     std::lock_guard<std::mutex> lock(mu);
     if (memo.size() > 4096) memo.clear();
     memo.emplace(key, p);
@@ -345,31 +400,43 @@ const Occupancy &occupancy(bool vec) {
     return table[dev][vec];
 }
 
+// The operands of one launch: a problem, or a block of rows and columns of
+// one (pointers at its first row and column, the stored row strides).
+struct Ops {
+    const float *A;
+    int lda;
+    long long sA;
+    const float *B;
+    int ldb;
+    long long sB;
+    float *C;
+    int ldc;
+    long long sC;
+};
+
 template <bool TA, bool TB, class Tile, int EPI>
-void launch_tile(int batch, int M, int N, int K, float alpha, const float *A, int lda,
-                 long long sA, const float *B, long long sB, float beta,
-                 float *C, long long sC, hipStream_t stream, bool vec, bmb::EpiArgs ep) {
+void launch_tile(int batch, int M, int N, int K, float alpha, const Ops &o, float beta,
+                 hipStream_t stream, bool vec, bmb::EpiArgs ep) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, batch);
     if (vec) {
         bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, true, EPI>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, alpha, A, lda, sA, B, sB, beta, C,
-                    sC, tiles_m, tiles_n, ep);
+                    L::SMEM_BYTES, stream, M, N, K, alpha, o.A, o.lda, o.sA, o.B, o.ldb, o.sB,
+                    beta, o.C, o.ldc, o.sC, tiles_m, tiles_n, ep);
     } else {
         bmb::allow_smem(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_k<TA, TB, Tile, false, EPI>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, alpha, A, lda, sA, B, sB, beta, C,
-                    sC, tiles_m, tiles_n, ep);
+                    L::SMEM_BYTES, stream, M, N, K, alpha, o.A, o.lda, o.sA, o.B, o.ldb, o.sB,
+                    beta, o.C, o.ldc, o.sC, tiles_m, tiles_n, ep);
     }
 }
 
 // A tile as KS k-slices of one workgroup (EPI_BLAS only).
 template <bool TA, bool TB, class Tile, int EPI, int KS>
-void launch_tile_ks(int batch, int M, int N, int K, float alpha, const float *A, int lda,
-                    long long sA, const float *B, long long sB, float beta, float *C,
-                    long long sC, hipStream_t stream, bool vec) {
+void launch_tile_ks(int batch, int M, int N, int K, float alpha, const Ops &o, float beta,
+                    hipStream_t stream, bool vec) {
     if constexpr (EPI == bmb::EPI_BLAS) {
         using L = bmb::MfmaLayout<TA, TB, Tile>;
         const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
@@ -378,13 +445,15 @@ void launch_tile_ks(int batch, int M, int N, int K, float alpha, const float *A,
         if (vec) {
             auto k = bmb::mfma_gemm_ks_k<TA, TB, Tile, true, EPI, KS>;
             bmb::allow_smem(k, smem);
-            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, A, lda, sA,
-                        B, sB, beta, C, sC, tiles_m, tiles_n, bmb::EpiArgs{});
+            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, o.A, o.lda,
+                        o.sA, o.B, o.ldb, o.sB, beta, o.C, o.ldc, o.sC, tiles_m, tiles_n,
+                        bmb::EpiArgs{});
         } else {
             auto k = bmb::mfma_gemm_ks_k<TA, TB, Tile, false, EPI, KS>;
             bmb::allow_smem(k, smem);
-            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, A, lda, sA,
-                        B, sB, beta, C, sC, tiles_m, tiles_n, bmb::EpiArgs{});
+            bmb::launch(k, grid, dim3(Tile::NT * KS), smem, stream, M, N, K, alpha, o.A, o.lda,
+                        o.sA, o.B, o.ldb, o.sB, beta, o.C, o.ldc, o.sC, tiles_m, tiles_n,
+                        bmb::EpiArgs{});
         }
     }
 }
@@ -392,36 +461,36 @@ void launch_tile_ks(int batch, int M, int N, int K, float alpha, const float *A,
 // Split-K: the partial sums of each K range go to P (splits x M x N), then
 // one reduce kernel adds them in range order and applies the epilogue.
 template <bool TA, bool TB, class Tile, int EPI>
-void launch_split(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
-                  const float *B, float beta, float *C, float *P, bool vec, bmb::EpiArgs ep,
-                  hipStream_t stream) {
+void launch_split(const Part &p, int M, int N, int K, float alpha, const Ops &o, float beta,
+                  float *P, bool vec, bmb::EpiArgs ep, hipStream_t stream) {
     using L = bmb::MfmaLayout<TA, TB, Tile>;
     const int tiles_m = bmb::ceil_div(M, Tile::BM), tiles_n = bmb::ceil_div(N, Tile::BN);
     const dim3 grid(tiles_m * tiles_n, p.splits);
     if (vec) {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, true>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, A, lda, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, o.A, o.lda, o.B, o.ldb, P, tiles_m, tiles_n,
+                    p.kchunk);
     } else {
         bmb::allow_smem(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, L::SMEM_BYTES);
         bmb::launch(bmb::mfma_gemm_splitk_k<TA, TB, Tile, false>, grid, dim3(Tile::NT),
-                    L::SMEM_BYTES, stream, M, N, K, A, lda, B, P, tiles_m, tiles_n, p.kchunk);
+                    L::SMEM_BYTES, stream, M, N, K, o.A, o.lda, o.B, o.ldb, P, tiles_m, tiles_n,
+                    p.kchunk);
     }
     const long long mn = (long long)M * N;
     bmb::launch(bmb::splitk_reduce_k<EPI>, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0,
-                stream, C, (const float *)P, p.splits, mn, N, alpha, beta, ep);
+                stream, o.C, (const float *)P, p.splits, mn, N, o.ldc, alpha, beta, ep);
 }
 
 template <bool TA, bool TB, int EPI>
-void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const float *A,
-              int lda, long long sA, const float *B, long long sB, float beta, float *C,
-              long long sC, float *P, bool vec, bmb::EpiArgs ep, hipStream_t stream) {
+void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const Ops &o,
+              float beta, float *P, bool vec, bmb::EpiArgs ep, hipStream_t stream) {
     if (p.splits > 1) {
         switch (CANDS[p.tile].kind) {
-        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
-        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, P, vec, ep, stream); break;
+        case TileKind::L: launch_split<TA, TB, TileL, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
+        case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
+        case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
+        case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
         }
         return;
     }
@@ -429,32 +498,24 @@ void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const 
         const int ks = CANDS[p.tile].ks;
         switch (CANDS[p.tile].kind) {
         case TileKind::M:
-            launch_tile_ks<TA, TB, TileM, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            launch_tile_ks<TA, TB, TileM, EPI, 2>(batch, M, N, K, alpha, o, beta, stream, vec);
             break;
         case TileKind::N:
-            if (ks == 2) launch_tile_ks<TA, TB, TileN, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
-            else launch_tile_ks<TA, TB, TileN, EPI, 4>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            if (ks == 2) launch_tile_ks<TA, TB, TileN, EPI, 2>(batch, M, N, K, alpha, o, beta, stream, vec);
+            else launch_tile_ks<TA, TB, TileN, EPI, 4>(batch, M, N, K, alpha, o, beta, stream, vec);
             break;
         default:
-            if (ks == 2) launch_tile_ks<TA, TB, TileS, EPI, 2>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
-            else launch_tile_ks<TA, TB, TileS, EPI, 4>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec);
+            if (ks == 2) launch_tile_ks<TA, TB, TileS, EPI, 2>(batch, M, N, K, alpha, o, beta, stream, vec);
+            else launch_tile_ks<TA, TB, TileS, EPI, 4>(batch, M, N, K, alpha, o, beta, stream, vec);
             break;
         }
         return;
     }
     switch (CANDS[p.tile].kind) {
-    case TileKind::L:
-        launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::M:
-        launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::N:
-        launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
-    case TileKind::S:
-        launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, A, lda, sA, B, sB, beta, C, sC, stream, vec, ep);
-        break;
+    case TileKind::L: launch_tile<TA, TB, TileL, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
+    case TileKind::M: launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
+    case TileKind::N: launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
+    case TileKind::S: launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
     }
 }
 
@@ -481,10 +542,18 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
     const bool may_split = batch == 1 && (fixed != nullptr || !bmb::stream_capturing(stream));
     Plan p = pick<TA, TB, EPI>(M, N, K, batch, vec, may_split, occ,
                                fixed ? fixed_floats : MAX_SPLIT_FLOATS);
-    long long pf = 0;
-    if (p.part[0].splits > 1) pf = (long long)p.part[0].splits * p.m1 * N;
-    if (p.m1 < M && p.part[1].splits > 1)
-        pf = std::max(pf, (long long)p.part[1].splits * (M - p.m1) * N);
+    // Partials: the largest split band's splits x rows x columns.
+    auto partials = [&](const Plan &q) {
+        long long pf = 0;
+        if (q.part[0].splits > 1) pf = (long long)q.part[0].splits * q.m1 * q.n1;
+        if (q.edges) return std::max(pf, bmb::edge_partial_floats(M - q.m1, N - q.n1, N, K));
+        if (q.m1 < M && q.part[1].splits > 1)
+            pf = std::max(pf, (long long)q.part[1].splits * (M - q.m1) * N);
+        if (q.n1 < N && q.part[2].splits > 1)
+            pf = std::max(pf, (long long)q.part[2].splits * q.m1 * (N - q.n1));
+        return pf;
+    };
+    const long long pf = partials(p);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
     if (pf > 0 && fixed == nullptr) {
@@ -492,18 +561,40 @@ void dispatch(int batch, int M, int N, int K, float alpha, const float *A,
         P = static_cast<float *>(lease->get());
         if (P == nullptr) p = pick<TA, TB, EPI>(M, N, K, batch, vec, false, occ);  // no split
     }
-    const int lda = TA ? M : K;
-    run_band<TA, TB, EPI>(p.part[0], batch, p.m1, N, K, alpha, A, lda, sA, B, sB, beta, C, sC,
-                          P, vec, ep, stream);
+    const int lda = TA ? M : K, ldb = TB ? K : N, ldc = N;
+    const Ops whole{A, lda, sA, B, ldb, sB, C, ldc, sC};
+    run_band<TA, TB, EPI>(p.part[0], batch, p.m1, p.n1, K, alpha, whole, beta, P, vec, ep,
+                          stream);
+    if (p.edges) {
+        bmb::gemm_edges(false, M, N, K, p.m1, p.n1, alpha, A, lda, B, ldb, beta, C, ldc, P,
+                        stream);
+        return;
+    }
+    if (p.n1 < N) {
+        // The right edge of the first rows: B and C n1 columns (TB: B n1
+        // rows) in, bias n1 entries in.
+        const size_t c = (size_t)p.n1;
+        Ops o = whole;
+        o.B = TB ? B + c * ldb : B + c;
+        o.C = C + c;
+        bmb::EpiArgs e = ep;
+        if (e.bias) e.bias += c;
+        if (e.act) e.act += c;
+        if (e.pre) e.pre += c;
+        run_band<TA, TB, EPI>(p.part[2], 1, p.m1, N - p.n1, K, alpha, o, beta, P,
+                              vec && al16(o.B), e, stream);
+    }
     if (p.m1 >= M) return;
     const size_t r = (size_t)p.m1;
     bmb::EpiArgs e1 = ep;
-    if (e1.act) e1.act += r * N;
-    if (e1.pre) e1.pre += r * N;
+    if (e1.act) e1.act += r * ldc;
+    if (e1.pre) e1.pre += r * ldc;
     // A band of rows starts r rows (TA: r columns of the stored K x M) in.
-    const float *A1 = TA ? A + r : A + r * K;
-    run_band<TA, TB, EPI>(p.part[1], 1, M - p.m1, N, K, alpha, A1, lda, sA, B, sB, beta,
-                          C + r * N, sC, P, vec && al16(A1), e1, stream);
+    Ops o = whole;
+    o.A = TA ? A + r : A + r * K;
+    o.C = C + r * ldc;
+    run_band<TA, TB, EPI>(p.part[1], 1, M - p.m1, N, K, alpha, o, beta, P, vec && al16(o.A), e1,
+                          stream);
 }
 
 void gemm_any(bool ta, bool tb, int batch, int M, int N, int K, float alpha,
@@ -571,30 +662,30 @@ void bmb::gemm_gelu_grad_nn(int M, int N, int K, const float *A, const float *B,
 void bmb::splitk_reduce(float *C, const float *P, int splits, long long mn, int N, float alpha,
                         float beta, hipStream_t stream) {
     bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BLAS>, dim3((unsigned)((mn + 1023) / 1024)),
-                dim3(256), 0, stream, C, P, splits, mn, N, alpha, beta, bmb::EpiArgs{});
+                dim3(256), 0, stream, C, P, splits, mn, N, N, alpha, beta, bmb::EpiArgs{});
 }
 
 void bmb::splitk_reduce_epi(int epi, float *C, const float *P, int splits, long long mn, int N,
-                            float alpha, float beta, hipStream_t stream, const float *bias,
-                            float *act, const float *pre) {
+                            int ldc, float alpha, float beta, hipStream_t stream,
+                            const float *bias, float *act, const float *pre) {
     const dim3 grid((unsigned)((mn + 1023) / 1024)), block(256);
     const bmb::EpiArgs ep{bias, act, pre};
     switch (epi) {
     case bmb::EPI_BIAS:
         bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BIAS>, grid, block, 0, stream, C, P, splits,
-                    mn, N, alpha, beta, ep);
+                    mn, N, ldc, alpha, beta, ep);
         break;
     case bmb::EPI_BIAS_GELU:
         bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BIAS_GELU>, grid, block, 0, stream, C, P,
-                    splits, mn, N, alpha, beta, ep);
+                    splits, mn, N, ldc, alpha, beta, ep);
         break;
     case bmb::EPI_GELU_GRAD:
         bmb::launch(bmb::splitk_reduce_k<bmb::EPI_GELU_GRAD>, grid, block, 0, stream, C, P,
-                    splits, mn, N, alpha, beta, ep);
+                    splits, mn, N, ldc, alpha, beta, ep);
         break;
     default:
         bmb::launch(bmb::splitk_reduce_k<bmb::EPI_BLAS>, grid, block, 0, stream, C, P, splits, mn,
-                    N, alpha, beta, ep);
+                    N, ldc, alpha, beta, ep);
         break;
     }
 }

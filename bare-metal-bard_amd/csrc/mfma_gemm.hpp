@@ -350,8 +350,8 @@ struct MfmaGemm {
     __device__ static __forceinline__ void run_tile(int M, int N, int K, int lda, int ldb,
                                                     float alpha, const float *__restrict__ A,
                                                     const float *__restrict__ B, float beta,
-                                                    float *C, int m0, int n0, float *smem,
-                                                    EpiArgs ep, int mlo, int nlo) {
+                                                    float *C, int ldc, int m0, int n0,
+                                                    float *smem, EpiArgs ep, int mlo, int nlo) {
         constexpr int G = BK / 8;  // 8-k groups per tile (even)
         constexpr bool INTERIOR = MODE != 0;             // no M / N bounds checks
         constexpr bool HINTED = MODE == 1 && HINTS;      // branch-free loop: scheduling hints
@@ -475,10 +475,10 @@ struct MfmaGemm {
         }
 
         if (INTERIOR && SHIFT<EPI> && (mlo > m0 || nlo > n0))
-            epilogue<EPI, INTERIOR, SHIFT<EPI>>(M, N, alpha, beta, C, m0, n0, ep, mlo, nlo, wm, wn,
-                                                lane, acc);
+            epilogue<EPI, INTERIOR, SHIFT<EPI>>(M, N, alpha, beta, C, ldc, m0, n0, ep, mlo, nlo, wm,
+                                                wn, lane, acc);
         else
-            epilogue<EPI, INTERIOR, false>(M, N, alpha, beta, C, m0, n0, ep, mlo, nlo, wm, wn,
+            epilogue<EPI, INTERIOR, false>(M, N, alpha, beta, C, ldc, m0, n0, ep, mlo, nlo, wm, wn,
                                            lane, acc);
     }
 
@@ -489,10 +489,11 @@ struct MfmaGemm {
     // are in flight at once; read-use-store per element would cost one memory
     // round trip per output. Same arithmetic as store_out. WIN: a shifted edge
     // tile, storing only rows >= mlo and columns >= nlo (it may read the
-    // others: they are inside C).
+    // others: they are inside C). C's rows (and those of ep.act and ep.pre)
+    // are ldc floats apart.
     template <int EPI, bool INTERIOR, bool WIN>
     __device__ static __forceinline__ void epilogue(int M, int N, float alpha, float beta,
-                                                    float *C, int m0, int n0, EpiArgs ep,
+                                                    float *C, int ldc, int m0, int n0, EpiArgs ep,
                                                     int mlo, int nlo, int wm, int wn, int lane,
                                                     const f32x16 (&acc)[FM][FN]) {
         const int l32 = lane & 31, half = lane >> 5;
@@ -509,7 +510,7 @@ struct MfmaGemm {
                     for (int r = 0; r < 16; ++r) {
                         const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                         in[fn][r] = (INTERIOR || (row < M && col < N))
-                                        ? src[(size_t)row * N + col] : 0.0f;
+                                        ? src[(size_t)row * ldc + col] : 0.0f;
                     }
                 }
             }
@@ -524,7 +525,7 @@ struct MfmaGemm {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (!INTERIOR && row >= M) continue;
                     if (WIN && row < mlo) continue;
-                    const size_t idx = (size_t)row * N + col;
+                    const size_t idx = (size_t)row * ldc + col;
                     const float a = acc[fi][fn][r];
                     float v;
                     if (EPI == EPI_PARTIAL) {
@@ -550,7 +551,7 @@ struct MfmaGemm {
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb,
                                                float alpha, const float *__restrict__ A,
                                                const float *__restrict__ B, float beta,
-                                               float *C, int m0, int n0, float *smem,
+                                               float *C, int ldc, int m0, int n0, float *smem,
                                                EpiArgs ep = {}) {
         // A partial tile at the bottom or right edge of a C at least one tile
         // large is shifted back to end at the edge, overlapping its
@@ -561,34 +562,35 @@ struct MfmaGemm {
         if (SHIFT<EPI> ? (M >= BM && N >= BN && K > 0) : (m0 + BM <= M && n0 + BN <= N && K > 0)) {
             const int ms = min(m0, M - BM), ns = min(n0, N - BN);
             if (K % (BK * KS) == 0)
-                run_tile<EPI, 1, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0,
-                                     n0);
+                run_tile<EPI, 1, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ldc, ms, ns, smem, ep,
+                                     m0, n0);
             else
-                run_tile<EPI, 2, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ms, ns, smem, ep, m0,
-                                     n0);
+                run_tile<EPI, 2, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ldc, ms, ns, smem, ep,
+                                     m0, n0);
         } else {
-            run_tile<EPI, 0, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, m0, n0, smem, ep, m0,
-                                 n0);
+            run_tile<EPI, 0, KS>(M, N, K, lda, ldb, alpha, A, B, beta, C, ldc, m0, n0, smem, ep,
+                                 m0, n0);
         }
     }
 };
 
 // Grid: x = output tiles (XCD-remapped, grouped), y = batch index. The
-// fused epilogues (EPI_BIAS*) are used for single problems only. lda: A's
-// row stride (at least M when TA, K otherwise), so that a band of rows of a
-// larger problem (A offset to its first row) runs as its own problem; B and
-// C are whole rows (ldb from K and N, C packed).
+// fused epilogues (EPI_BIAS*) are used for single problems only. lda, ldb,
+// ldc: the row strides of the stored A (at least M when TA, K otherwise), B
+// (at least K when TB, N otherwise) and C (at least N), so that a block of
+// rows and columns of a larger problem (its operands offset to its first row
+// and column) runs as a problem of its own.
 template <bool TA, bool TB, class Tile, bool VEC, int EPI>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
     int M, int N, int K, float alpha, const float *__restrict__ A, int lda,
-    long long sA, const float *__restrict__ B, long long sB, float beta,
-    float *C, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
+    long long sA, const float *__restrict__ B, int ldb, long long sB, float beta,
+    float *C, int ldc, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
     extern __shared__ float smem_dyn[];
     const size_t z = blockIdx.y;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, lda, TB ? K : N, alpha,
-                                                   A + z * sA, B + z * sB, beta, C + z * sC,
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI>(M, N, K, lda, ldb, alpha, A + z * sA,
+                                                   B + z * sB, beta, C + z * sC, ldc,
                                                    tm * Tile::BM, tn * Tile::BN, smem_dyn, ep);
 }
 
@@ -597,14 +599,14 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_k(
 template <bool TA, bool TB, class Tile, bool VEC, int EPI, int KS>
 __global__ __launch_bounds__(Tile::NT * KS) void mfma_gemm_ks_k(
     int M, int N, int K, float alpha, const float *__restrict__ A, int lda,
-    long long sA, const float *__restrict__ B, long long sB, float beta,
-    float *C, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
+    long long sA, const float *__restrict__ B, int ldb, long long sB, float beta,
+    float *C, int ldc, long long sC, int tiles_m, int tiles_n, EpiArgs ep) {
     extern __shared__ float smem_dyn[];
     const size_t z = blockIdx.y;
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
-    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI, KS>(M, N, K, lda, TB ? K : N, alpha,
-                                                       A + z * sA, B + z * sB, beta, C + z * sC,
+    MfmaGemm<TA, TB, Tile, VEC>::template run<EPI, KS>(M, N, K, lda, ldb, alpha, A + z * sA,
+                                                       B + z * sB, beta, C + z * sC, ldc,
                                                        tm * Tile::BM, tn * Tile::BN, smem_dyn,
                                                        ep);
 }
@@ -616,7 +618,7 @@ __global__ __launch_bounds__(Tile::NT * KS) void mfma_gemm_ks_k(
 template <bool TA, bool TB, class Tile, bool VEC>
 __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
     int M, int N, int K, const float *__restrict__ A, int lda, const float *__restrict__ B,
-    float *P, int tiles_m, int tiles_n, int kchunk) {
+    int ldb, float *P, int tiles_m, int tiles_n, int kchunk) {
     extern __shared__ float smem_dyn[];
     const int s = blockIdx.y;
     const int kb = s * kchunk;
@@ -624,22 +626,24 @@ __global__ __launch_bounds__(Tile::NT) void mfma_gemm_splitk_k(
     int tm, tn;
     group_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const float *As = TA ? A + (size_t)kb * lda : A + kb;
-    const float *Bs = TB ? B + kb : B + (size_t)kb * N;
+    const float *Bs = TB ? B + kb : B + (size_t)kb * ldb;
     MfmaGemm<TA, TB, Tile, VEC>::template run<EPI_PARTIAL>(
-        M, N, klen, lda, TB ? K : N, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N,
+        M, N, klen, lda, ldb, 1.0f, As, Bs, 0.0f, P + (size_t)s * M * N, N,
         tm * Tile::BM, tn * Tile::BN, smem_dyn);
 }
 
 // C = epilogue of sum_{s < splits} P[s]: one float4 of C per lane, splits
 // added in ascending order, so the result depends only on the shape. N is
-// the row length (for the bias column of an element).
+// the row length of the packed partials (and gives an element's bias
+// column); C's rows (and those of ep.act, ep.pre) are ldc floats apart.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_k(float *C, const float *P, int splits,
-                                                       long long mn, int N, float alpha,
-                                                       float beta, EpiArgs ep) {
+                                                       long long mn, int N, int ldc,
+                                                       float alpha, float beta, EpiArgs ep) {
     const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
-    const bool whole = i + 3 < mn;
+    const bool packed = ldc == N;
+    const bool whole = packed && i + 3 < mn;
     float acc[4];
     if (whole) {
         float4 v;
@@ -670,8 +674,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(float *C, const float *P,
     }
     for (int k = 0; k < 4; ++k) {
         if (i + k >= mn) break;
-        const float bias = (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) ? ep.bias[(i + k) % N] : 0.0f;
-        store_out<EPI>(C, ep, (size_t)(i + k), acc[k], alpha, beta, bias);
+        const long long row = (i + k) / N, col = (i + k) % N;
+        const float bias = (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) ? ep.bias[col] : 0.0f;
+        store_out<EPI>(C, ep, packed ? (size_t)(i + k) : (size_t)(row * ldc + col), acc[k], alpha,
+                       beta, bias);
     }
 }
 

@@ -48,6 +48,8 @@
 // barrier, converted at the same time while the matrix core idled. The fenced
 // order is 1-5% faster on the GPT-2 shapes and 2% at N = 4096, bit-identical.
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <map>
@@ -417,14 +419,17 @@ struct Bf16x3Gemm {
     }
 
     // One output tile over k in [0, K) (A, B positioned at that range's
-    // start). INTERIOR: the tile lies inside M x N and K is a positive whole
-    // number of stages, so no load or store needs a bounds check. EPI: what
-    // the epilogue stores (bmb::Epi; EPI_PARTIAL: the raw sums, row stride N).
-    template <bool INTERIOR, int EPI>
+    // start). INTERIOR: the tile lies inside M x N and K > 0, so no store
+    // and no load of a whole stage needs a bounds check. KTAIL (INTERIOR
+    // only): K is not a whole number of stages, and the last stage's loads
+    // are guarded (zero fill past K); every other stage runs the interior
+    // loop. EPI: what the epilogue stores (bmb::Epi; EPI_PARTIAL: the raw
+    // sums). C's rows (and those of ep.act, ep.pre) are ldc floats apart.
+    template <bool INTERIOR, int EPI, bool KTAIL = false>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb, float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B, float beta, float *C,
-                                               int m0, int n0, __bf16 *smem,
+                                               int ldc, int m0, int n0, __bf16 *smem,
                                                const bmb::EpiArgs &ep) {
         const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tl::WAVES_N) * Tl::WM, wn = (wave % Tl::WAVES_N) * Tl::WN;
@@ -453,7 +458,7 @@ struct Bf16x3Gemm {
             return TB ? B + (size_t)n0 * ldb + (size_t)kt * BK : B + (size_t)kt * BK * ldb + n0;
         };
         auto load = [&](int kt) {
-            if (INTERIOR) {
+            if (INTERIOR && !(KTAIL && kt == nkt - 1)) {
                 ga.load_interior(a_at(kt), oa, tid);
                 gb.load_interior(b_at(kt), ob, tid);
             } else {
@@ -473,8 +478,9 @@ struct Bf16x3Gemm {
         __syncthreads();
         int kt0 = 0;
         if (INTERIOR) {
-            // Stages with a next stage to store and a stage after it to load.
-            for (; kt0 + 2 < nkt; ++kt0) {
+            // Stages with a next stage to store and a whole stage after it to
+            // load (KTAIL: the last stage is loaded by the loop below).
+            for (; kt0 + 2 < nkt - (KTAIL ? 1 : 0); ++kt0) {
                 const __bf16 *st = smem + (kt0 & 1) * Tl::STAGE;
                 step0_fused(st, smem + ((kt0 + 1) & 1) * Tl::STAGE, ga, gb, a_at(kt0 + 2),
                             b_at(kt0 + 2), oa, ob, wm, wn, lane, tid, acc);
@@ -519,7 +525,7 @@ struct Bf16x3Gemm {
                     for (int r = 0; r < 16; ++r) {
                         const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                         in[fn][r] = (INTERIOR || (row < M && col < N))
-                                        ? src[(size_t)row * N + col] : 0.0f;
+                                        ? src[(size_t)row * ldc + col] : 0.0f;
                     }
                 }
             }
@@ -532,7 +538,7 @@ struct Bf16x3Gemm {
                     const int row = m0 + wm + fi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     if (!INTERIOR && row >= M) continue;
                     const float a = acc[fi][fn][r];
-                    const size_t idx = (size_t)row * N + col;
+                    const size_t idx = (size_t)row * ldc + col;
                     if (EPI == bmb::EPI_PARTIAL) {
                         C[idx] = a;
                     } else if (EPI == bmb::EPI_BLAS) {
@@ -552,30 +558,36 @@ struct Bf16x3Gemm {
 
 // Grid: x = output tiles (XCD-remapped, grouped), y = K range s, covering
 // k in [s*kchunk, min(K, (s+1)*kchunk)) (kchunk a multiple of BK when
-// gridDim.y > 1). EPI_PARTIAL: write the range's raw sums to C + s*M*N.
-// lda: A's row stride (at least M when TA, K otherwise), so that a band of
-// rows of a larger problem (A offset to its first row) runs as its own
-// problem; B and C are whole rows (ldb from K and N, C packed).
+// gridDim.y > 1). EPI_PARTIAL: write the range's raw sums to C + s*M*N
+// (packed rows). lda, ldb, ldc: the row strides of the stored A (at least M
+// when TA, K otherwise), B (at least K when TB, N otherwise) and C (at least
+// N), so that a block of rows and columns of a larger problem (its operands
+// offset to its first row and column) runs as a problem of its own.
 template <class Tl, bool TA, bool TB, bool VEC, int EPI>
 __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchunk, float alpha,
                                                    const float *__restrict__ A, int lda,
-                                                   const float *__restrict__ B, float beta,
-                                                   float *C, int tiles_m, int tiles_n,
-                                                   bmb::EpiArgs ep) {
+                                                   const float *__restrict__ B, int ldb,
+                                                   float beta, float *C, int ldc, int tiles_m,
+                                                   int tiles_n, bmb::EpiArgs ep) {
     extern __shared__ __bf16 lds[];
     using G = Bf16x3Gemm<Tl, TA, TB, VEC>;
     int tm, tn;
     bmb::group_tile(bmb::xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
     const int m0 = tm * Tl::BM, n0 = tn * Tl::BN;
-    const int ldb = TB ? K : N;
     const int kb = blockIdx.y * kchunk, klen = min(K, kb + kchunk) - kb;
     const float *Ak = TA ? A + (size_t)kb * lda : A + kb;
     const float *Bk = TB ? B + kb : B + (size_t)kb * ldb;
     float *Cs = EPI == bmb::EPI_PARTIAL ? C + (size_t)blockIdx.y * M * N : C;
+    const int ldcs = EPI == bmb::EPI_PARTIAL ? N : ldc;
     if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0 && klen % BK == 0)
-        G::template run<true, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, m0, n0, lds, ep);
+        G::template run<true, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, ldcs, m0, n0,
+                                   lds, ep);
+    else if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0)
+        G::template run<true, EPI, true>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, ldcs, m0,
+                                         n0, lds, ep);
     else
-        G::template run<false, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, m0, n0, lds, ep);
+        G::template run<false, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, ldcs, m0, n0,
+                                    lds, ep);
 }
 
 // ------------------------------------------------------------- host side
@@ -654,9 +666,16 @@ struct Part {
 };
 
 // Rows [0, m1) run on part[0], rows [m1, M) on part[1] (m1 == M: one band).
+// A corner plan (edges) instead runs rows [0, m1) x columns [0, n1) on
+// part[0], a block of whole tiles, and the at most EDGE_MAX columns right of
+// it and rows below it on the edge kernels (edge_gemm.hip): 4097^2 as
+// 4096^2 on 256 x 256 tiles plus a 4096 x 1 and a 1 x 4097 edge, where a
+// plan of tiles alone computes 289 tiles (13% more than C) or runs a second
+// band.
 struct Plan {
     Part part[2];
-    int m1;
+    int m1, n1;
+    bool edges;
 };
 
 struct Device {
@@ -737,9 +756,10 @@ double best_part(const Device &dv, int M, int N, int K, bool may_split, long lon
     return best_t;
 }
 
-Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats) {
+Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats,
+              bool edges_ok) {
     const Device &dv = device_info(dev);
-    Plan best{{Part{0, 1, K}, Part{0, 1, K}}, M};
+    Plan best{{Part{0, 1, K}, Part{0, 1, K}}, M, N, false};
     const double single_t = best_part(dv, M, N, K, may_split, max_floats, best.part[0]);
     double best_t = single_t;
     // Two bands: the first whole rounds of one tile, the rest on its own plan.
@@ -760,79 +780,108 @@ Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats
             const double tm = t0 + t1 + BAND_S;
             if (tm < BAND_GAIN * single_t && tm < best_t) {
                 best_t = tm;
-                best = Plan{{p0, p1}, m1};
+                best = Plan{{p0, p1}, m1, N, false};
             }
         }
     }
+    // Corner plans: whole tiles of one candidate over [0, m1) x [0, n1), the
+    // edges on the edge kernels (row-major A and B, BLAS epilogue; their
+    // scratch only where K may be split).
+    for (int t = 0; edges_ok && may_split && K >= MIN_BAND_K && t < N_CANDS; ++t) {
+        const B3Cand &c = CANDS[t];
+        const int m1 = M / c.bm * c.bm, n1 = N / c.bn * c.bn;
+        if (m1 == 0 || n1 == 0 || (m1 == M && n1 == N) || M - m1 > bmb::EDGE_MAX ||
+            N - n1 > bmb::EDGE_MAX || bmb::edge_partial_floats(M - m1, N - n1, N, K) > max_floats)
+            continue;
+        Part p0;
+        double t0;
+        if (!part_time(dv, m1, n1, K, t, 1, false, 0, p0, t0)) continue;
+        const double tm = t0 + bmb::edge_model_s(m1, N - n1, M - m1, N, K);
+        if (tm < BAND_GAIN * single_t && tm < best_t) {
+            best_t = tm;
+            best = Plan{{p0, Part{0, 1, K}}, m1, n1, true};
+        }
+    }
+    if (getenv("BMB_GEMM_PLAN_TRACE") != nullptr)
+        fprintf(stderr, "bf16x3 gemm plan %dx%dx%d: m1 %d n1 %d edges %d parts (%d,%d,%d) "
+                        "(%d,%d,%d) model %.1f us (one band %.1f us)\n",
+                M, N, K, best.m1, best.n1, (int)best.edges, best.part[0].tile,
+                best.part[0].splits, best.part[0].kchunk, best.part[1].tile, best.part[1].splits,
+                best.part[1].kchunk, best_t * 1e6, single_t * 1e6);
     return best;
 }
 
 // Plans are memoised per (device, shape, split permission and cap): the
 // search above costs tens of microseconds, a GEMM call in a training step
 // a few hundred.
-Plan pick(int M, int N, int K, bool may_split, long long max_floats) {
+Plan pick(int M, int N, int K, bool may_split, long long max_floats, bool edges_ok) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    using Key = std::tuple<int, int, int, int, bool, long long>;
+    using Key = std::tuple<int, int, int, int, bool, long long, bool>;
     static std::mutex mu;
     static std::map<Key, Plan> memo;
-    const Key key{dev, M, N, K, may_split, max_floats};
+    const Key key{dev, M, N, K, may_split, max_floats, edges_ok};
     {
         std::lock_guard<std::mutex> lock(mu);
         auto it = memo.find(key);
         if (it != memo.end()) return it->second;
     }
-    const Plan p = plan_for(dev, M, N, K, may_split, max_floats);
+    const Plan p = plan_for(dev, M, N, K, may_split, max_floats, edges_ok);
     std::lock_guard<std::mutex> lock(mu);
     if (memo.size() > 4096) memo.clear();
     memo.emplace(key, p);
     return p;
 }
 
+// The row strides of a launch's operands (see bf16x3_k).
+struct Strides {
+    int lda, ldb, ldc;
+};
+
 template <class Tl, bool TA, bool TB, int EPI>
-void launch(int M, int N, int K, int kchunk, int splits, float alpha, const float *A, int lda,
-            const float *B, float beta, float *C, bool vec, hipStream_t stream,
-            bmb::EpiArgs ep) {
+void launch(int M, int N, int K, int kchunk, int splits, float alpha, const float *A,
+            const float *B, float beta, float *C, const Strides &ld, bool vec,
+            hipStream_t stream, bmb::EpiArgs ep) {
     const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
     const dim3 grid(tiles_m * tiles_n, splits);
     if (vec) {
         auto kern = bf16x3_k<Tl, TA, TB, true, EPI>;
         bmb::allow_smem(kern, Tl::SMEM_BYTES);
         bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    lda, B, beta, C, tiles_m, tiles_n, ep);
+                    ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
     } else {
         auto kern = bf16x3_k<Tl, TA, TB, false, EPI>;
         bmb::allow_smem(kern, Tl::SMEM_BYTES);
         bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    lda, B, beta, C, tiles_m, tiles_n, ep);
+                    ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
     }
 }
 
 // One band on tile Tl: one launch with the epilogue, or the split partials
 // (EPI_PARTIAL into P) and the shared reduce with the epilogue.
 template <class Tl, bool TA, bool TB, int EPI>
-void run_part(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
-              const float *B, float beta, float *C, bool vec, float *P, hipStream_t stream,
+void run_part(const Part &p, int M, int N, int K, float alpha, const float *A, const float *B,
+              float beta, float *C, const Strides &ld, bool vec, float *P, hipStream_t stream,
               bmb::EpiArgs ep) {
     if (p.splits > 1) {
-        launch<Tl, TA, TB, bmb::EPI_PARTIAL>(M, N, K, p.kchunk, p.splits, 1.0f, A, lda, B, 0.0f,
-                                             P, vec, stream, ep);
-        bmb::splitk_reduce_epi(EPI, C, P, p.splits, (long long)M * N, N, alpha, beta, stream,
-                               ep.bias, ep.act, ep.pre);
+        launch<Tl, TA, TB, bmb::EPI_PARTIAL>(M, N, K, p.kchunk, p.splits, 1.0f, A, B, 0.0f, P,
+                                             ld, vec, stream, ep);
+        bmb::splitk_reduce_epi(EPI, C, P, p.splits, (long long)M * N, N, ld.ldc, alpha, beta,
+                               stream, ep.bias, ep.act, ep.pre);
     } else {
-        launch<Tl, TA, TB, EPI>(M, N, K, K, 1, alpha, A, lda, B, beta, C, vec, stream, ep);
+        launch<Tl, TA, TB, EPI>(M, N, K, K, 1, alpha, A, B, beta, C, ld, vec, stream, ep);
     }
 }
 
 template <bool TA, bool TB, int EPI>
-void run_band(const Part &p, int M, int N, int K, float alpha, const float *A, int lda,
-              const float *B, float beta, float *C, bool vec, float *P, hipStream_t stream,
+void run_band(const Part &p, int M, int N, int K, float alpha, const float *A, const float *B,
+              float beta, float *C, const Strides &ld, bool vec, float *P, hipStream_t stream,
               bmb::EpiArgs ep) {
     switch (p.tile) {
-    case 0: run_part<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
-    case 1: run_part<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
-    case 2: run_part<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
-    default: run_part<TileT, TA, TB, EPI>(p, M, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep); break;
+    case 0: run_part<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
+    case 1: run_part<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
+    case 2: run_part<TileS, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
+    default: run_part<TileT, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
     }
 }
 
@@ -841,8 +890,13 @@ void run_band(const Part &p, int M, int N, int K, float alpha, const float *A, i
 template <bool TA, bool TB, int EPI>
 void run_plan(const Plan &p, int M, int N, int K, float alpha, const float *A, const float *B,
               float beta, float *C, bool vec, float *P, hipStream_t stream, bmb::EpiArgs ep) {
-    const int lda = TA ? M : K;
-    run_band<TA, TB, EPI>(p.part[0], p.m1, N, K, alpha, A, lda, B, beta, C, vec, P, stream, ep);
+    const Strides ld{TA ? M : K, TB ? K : N, N};
+    run_band<TA, TB, EPI>(p.part[0], p.m1, p.n1, K, alpha, A, B, beta, C, ld, vec, P, stream, ep);
+    if (p.edges) {
+        bmb::gemm_edges(true, M, N, K, p.m1, p.n1, alpha, A, ld.lda, B, ld.ldb, beta, C, ld.ldc,
+                        P, stream);
+        return;
+    }
     if (p.m1 >= M) return;
     const size_t r = (size_t)p.m1;
     bmb::EpiArgs e1 = ep;
@@ -852,12 +906,13 @@ void run_plan(const Plan &p, int M, int N, int K, float alpha, const float *A, c
     const float *A1 = TA ? A + r : A + r * K;
     // 16-byte loads of the band need its first row aligned as well.
     const bool vec1 = vec && (((uintptr_t)A1 & 15) == 0);
-    run_band<TA, TB, EPI>(p.part[1], M - p.m1, N, K, alpha, A1, lda, B, beta, C + r * N, vec1,
-                          P, stream, e1);
+    run_band<TA, TB, EPI>(p.part[1], M - p.m1, N, K, alpha, A1, B, beta, C + r * N, ld, vec1, P,
+                          stream, e1);
 }
 
-long long partial_floats(const Plan &p, int M, int N) {
+long long partial_floats(const Plan &p, int M, int N, int K) {
     long long f = 0;
+    if (p.edges) return bmb::edge_partial_floats(M - p.m1, N - p.n1, N, K);
     if (p.part[0].splits > 1) f = (long long)p.part[0].splits * p.m1 * N;
     if (p.m1 < M && p.part[1].splits > 1)
         f = std::max(f, (long long)p.part[1].splits * (M - p.m1) * N);
@@ -884,14 +939,15 @@ bool bmb::bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const 
     const bool vec = a_contig % 4 == 0 && b_contig % 4 == 0 && (((uintptr_t)A & 15) == 0) &&
                      (((uintptr_t)B & 15) == 0);
     const bool may_split = fixed != nullptr || !bmb::stream_capturing(stream);
-    Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS);
+    const bool edges_ok = !ta && !tb && epi == bmb::EPI_BLAS;
+    Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS, edges_ok);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
-    const long long pf = partial_floats(p, M, N);
+    const long long pf = partial_floats(p, M, N, K);
     if (pf > 0 && fixed == nullptr) {
         lease.emplace(bmb::SCRATCH_GEMM, (size_t)pf * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
-        if (P == nullptr) p = pick(M, N, K, false, 0);  // no scratch: no split
+        if (P == nullptr) p = pick(M, N, K, false, 0, edges_ok);  // no scratch: no split
     }
 #define BMB_B3(TA_, TB_, EPI_)                                                              \
     run_plan<TA_, TB_, EPI_>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep);         \

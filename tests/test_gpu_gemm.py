@@ -467,3 +467,51 @@ def test_row_bands(gpu, trans, math):
         assert e3 < bound, (e3, bound)
     else:
         assert err < fp32_order_bound(K), err
+
+
+# ---- corner plans: C as a block of whole 256 x 256 tiles plus at most 8
+# columns right of it and 8 rows below it, the edges on the edge kernels
+# (edge_gemm.hip; row-major A and B, BLAS epilogue). The plan trace
+# (BMB_GEMM_PLAN_TRACE, read when a shape is first planned) shows that these
+# shapes take that plan; the sampled rows include every edge row, and every
+# sampled row is checked over all columns (the right edge included). The
+# fp32 mode's edges use exact fp32 products, the bf16x3 mode's the bf16x3
+# split's three products, each held to its own bound.
+
+# (distinct shapes per mode: plans are memoised per shape; the last has only
+# a right edge)
+@pytest.mark.parametrize("shape,math", [((4104, 4101, 4099), 0), ((4097, 4100, 4096), 0),
+                                        ((4103, 4101, 4099), 1), ((4096, 4100, 4096), 1)],
+                         ids=["4104x4101x4099-bf16x3", "4097x4100x4096-bf16x3",
+                              "4103x4101x4099-fp32", "4096x4100x4096-fp32"])
+def test_corner_edges(gpu, shape, math, capfd, monkeypatch):
+    M, N, K = shape
+    A = O.fill_xorshift(M * K, 0x6161)
+    B = O.fill_xorshift(K * N, 0x7171)
+    C0 = O.fill_xorshift(M * N, 0x8181)
+    monkeypatch.setenv("BMB_GEMM_PLAN_TRACE", "1")
+    with bmb.gemm_math(math):
+        dA, dB, dC = dev(A), dev(B), dev(C0)
+        print("gemm NN %dx%dx%d math %d" % (M, N, K, math), flush=True)
+        bmb.gemm(False, False, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 1.25, dC.data_ptr())
+        sync("gemm corner edges")
+    err_out = capfd.readouterr().err
+    plan = [l for l in err_out.splitlines() if "gemm plan %dx%dx%d:" % (M, N, K) in l]
+    assert plan and "edges 1" in plan[0], err_out
+    m1 = M // 256 * 256
+    got = dC.cpu().numpy().reshape(M, N)
+    rows = np.unique(np.r_[0, 1, 255, 256, 2047, 2048, m1 - 1, np.arange(m1, M), M - 1])
+    Aop = A.reshape(M, K)[rows]
+    c0 = C0.reshape(M, N)[rows]
+    ref = O.gemm_f64(False, False, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+    err, bad = O.normwise(got[rows], ref)
+    assert bad == 0 and err < 1e-4
+    if math == 0:
+        e3, bound = bf16x3_err(got[rows], False, False, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+        assert e3 < bound, (e3, bound)
+    else:
+        assert err < fp32_order_bound(K), err
+    # the edge columns alone, over the sampled rows
+    n1 = N // 256 * 256
+    e_edge, bad = O.normwise(got[rows][:, n1:], ref[:, n1:])
+    assert bad == 0 and e_edge < (fp32_order_bound(3 * K) if math == 0 else fp32_order_bound(K))
