@@ -563,7 +563,11 @@ struct Bf16x3Gemm {
 // when TA, K otherwise), B (at least K when TB, N otherwise) and C (at least
 // N), so that a block of rows and columns of a larger problem (its operands
 // offset to its first row and column) runs as a problem of its own.
-template <class Tl, bool TA, bool TB, bool VEC, int EPI>
+// KT: K is not a whole number of stages; interior tiles then run the
+// interior loop with a guarded last stage (Bf16x3Gemm::run's KTAIL). A
+// separate instantiation: the extra path costs the 256 x 256 kernels about a
+// dozen spilled registers, which the other shapes need not pay.
+template <class Tl, bool TA, bool TB, bool VEC, int EPI, bool KT = false>
 __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchunk, float alpha,
                                                    const float *__restrict__ A, int lda,
                                                    const float *__restrict__ B, int ldb,
@@ -582,7 +586,7 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
     if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0 && klen % BK == 0)
         G::template run<true, EPI>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, ldcs, m0, n0,
                                    lds, ep);
-    else if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0)
+    else if (KT && m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen > 0)
         G::template run<true, EPI, true>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, Cs, ldcs, m0,
                                          n0, lds, ep);
     else
@@ -844,16 +848,21 @@ void launch(int M, int N, int K, int kchunk, int splits, float alpha, const floa
             hipStream_t stream, bmb::EpiArgs ep) {
     const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
     const dim3 grid(tiles_m * tiles_n, splits);
+    auto go = [&](auto kern) {
+        bmb::allow_smem(kern, Tl::SMEM_BYTES);
+        bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
+                    ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
+    };
+    // (A ragged K has the guarded-tail interior kernels for the BLAS and
+    // split-K epilogues; the fused ones run at K = 768 and 3072.)
+    constexpr bool KT_OK = EPI == bmb::EPI_BLAS || EPI == bmb::EPI_PARTIAL;
+    const bool kt = KT_OK && K % BK != 0;
     if (vec) {
-        auto kern = bf16x3_k<Tl, TA, TB, true, EPI>;
-        bmb::allow_smem(kern, Tl::SMEM_BYTES);
-        bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
+        if (kt) go(bf16x3_k<Tl, TA, TB, true, EPI, KT_OK>);
+        else go(bf16x3_k<Tl, TA, TB, true, EPI>);
     } else {
-        auto kern = bf16x3_k<Tl, TA, TB, false, EPI>;
-        bmb::allow_smem(kern, Tl::SMEM_BYTES);
-        bmb::launch(kern, grid, dim3(Tl::NT), Tl::SMEM_BYTES, stream, M, N, K, kchunk, alpha, A,
-                    ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
+        if (kt) go(bf16x3_k<Tl, TA, TB, false, EPI, KT_OK>);
+        else go(bf16x3_k<Tl, TA, TB, false, EPI>);
     }
 }
 
