@@ -8,14 +8,15 @@
 // sliver of A and all of B. On matrix-core tiles (64 wide at the least) nearly
 // all of their work would be padding; here the VALU streams the large operand
 // once, at HBM rate.
-//  - right: B's K x rn sliver is first packed into rn contiguous rows, then
-//    one wave per row of A, its lanes taking K in float4 steps, rn sums per
+//  - right: B's K x rn sliver is first packed into rn contiguous rows (for
+//    bf16x3, its split's hi and lo rows), then one wave per row of A, its lanes taking K in float4 steps, rn sums per
 //    lane, a fixed-order butterfly over the wave (every lane ends with the
 //    same bits), and the lanes j < rn store C[row][n1 + j];
 //  - bottom: one thread per 4 consecutive columns of B over one of `ranges`
 //    consecutive K ranges, rm x 4 sums per thread, stored as partials
-//    (ranges x rm x N); edge_reduce_k adds them in range order and applies
-//    the epilogue.
+//    (ranges x rm x N); edge_reduce_k adds them in a fixed order and applies
+//    the epilogue. Three launches: bottom partials (with the packing), right
+//    edge, reduce.
 // Every sum is an fp32 sum of exact products: fp32 products (the fp32 path),
 // or, for the bf16x3 path, the three bf16 products hi*hi + hi*lo + lo*hi of
 // the bf16x3 kernels' split, so an edge element meets the same bound as the
@@ -54,13 +55,30 @@ __device__ __forceinline__ float madd(float a, float ah, float al, float b, floa
 
 // B's right edge, K x rn floats rows ldb apart, packed to rn rows of K
 // (Bs[j K + k]), so that the right edge reads it as 128-bit loads: read in
-// place, every wave would touch one cache line per k for each 4 bytes.
-__global__ __launch_bounds__(256) void edge_pack_k(int K, int rn, const float *__restrict__ B,
-                                                   int ldb, float *__restrict__ Bs) {
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+// place, every wave would touch one cache line per k for each 4 bytes. BF:
+// the bf16x3 split's hi and lo of each value instead (Bs and Bs + rn K),
+// split once here rather than by every row's wave.
+template <bool BF>
+__device__ __forceinline__ void edge_pack(long long e, int K, int rn, const float *__restrict__ B,
+                                          int ldb, float *__restrict__ Bs) {
     if (e >= (long long)K * rn) return;
     const int j = (int)(e / K), k = (int)(e % K);
-    Bs[e] = B[(size_t)k * ldb + j];
+    const float b = B[(size_t)k * ldb + j];
+    if (BF) {
+        float hi, lo;
+        split_bf(b, hi, lo);
+        Bs[e] = hi;
+        Bs[(size_t)rn * K + e] = lo;
+    } else {
+        Bs[e] = b;
+    }
+}
+
+// The packing alone (no bottom edge to ride).
+template <bool BF>
+__global__ __launch_bounds__(256) void edge_pack_k(int K, int rn, const float *__restrict__ B,
+                                                   int ldb, float *__restrict__ Bs) {
+    edge_pack<BF>((long long)blockIdx.x * 256 + threadIdx.x, K, rn, B, ldb, Bs);
 }
 
 // Four consecutive floats of a row that may end inside them (zeros past n).
@@ -84,21 +102,23 @@ __global__ __launch_bounds__(256) void edge_right_k(int m1, int K, float alpha,
                                                     const float *__restrict__ A, int lda,
                                                     const float *__restrict__ Bs, float beta,
                                                     float *C, int ldc) {
-    constexpr int U = RN <= 2 ? 8 : RN <= 4 ? 4 : 2;
+    // (BF: Bs holds the split, hi rows then lo rows; twice the B loads per step.)
+    constexpr int U = (BF ? 2 : 1) * RN <= 2 ? 8 : (BF ? 2 : 1) * RN <= 4 ? 4 : 2;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= m1) return;  // (uniform over the wave)
     float acc[RN];
 #pragma unroll
     for (int j = 0; j < RN; ++j) acc[j] = 0.0f;
     const float *a = A + (size_t)row * lda;
+    constexpr int NB = BF ? 2 : 1;  // B rows per column: the value, or its hi and lo
     for (int k0 = lane * 4; k0 < K; k0 += 256 * U) {
-        float av[U][4], bv[U][RN][4];
+        float av[U][4], bv[U][NB * RN][4];
 #pragma unroll
         for (int s = 0; s < U; ++s) {
             const int k = k0 + 256 * s;
             load4_tail(a, k, K, av[s]);
 #pragma unroll
-            for (int j = 0; j < RN; ++j) load4_tail(Bs + (size_t)j * K, k, K, bv[s][j]);
+            for (int j = 0; j < NB * RN; ++j) load4_tail(Bs + (size_t)j * K, k, K, bv[s][j]);
         }
 #pragma unroll
         for (int s = 0; s < U; ++s)
@@ -109,8 +129,7 @@ __global__ __launch_bounds__(256) void edge_right_k(int m1, int K, float alpha,
 #pragma unroll
                 for (int j = 0; j < RN; ++j) {
                     const float b = bv[s][j][u];
-                    float bh = 0.0f, bl = 0.0f;
-                    if (BF) split_bf(b, bh, bl);
+                    const float bh = BF ? b : 0.0f, bl = BF ? bv[s][RN + j][u] : 0.0f;
                     acc[j] = madd<BF>(av[s][u], ah, al, b, bh, bl, acc[j]);
                 }
             }
@@ -133,12 +152,20 @@ __global__ __launch_bounds__(256) void edge_right_k(int m1, int K, float alpha,
 // workgroup (cb, r) takes columns 4 (cb 256 + t) .. + 3 over K range r, U
 // rows of B loaded ahead of their multiplies. Zeros past K (the zero rows
 // add nothing).
+// Workgroups past ncb * ranges pack B's right edge (edge_pack) instead, so
+// that the packing rides this launch.
 template <bool BF, int RM>
-__global__ __launch_bounds__(256) void edge_bottom_k(int N, int K, int kr, int ncb,
+__global__ __launch_bounds__(256) void edge_bottom_k(int N, int K, int kr, int ncb, int nbot,
                                                      const float *__restrict__ A, int lda,
                                                      const float *__restrict__ B, int ldb,
-                                                     float *__restrict__ P) {
+                                                     float *__restrict__ P, int rn,
+                                                     const float *__restrict__ Bn,
+                                                     float *__restrict__ Bs) {
     constexpr int U = 8;
+    if ((int)blockIdx.x >= nbot) {
+        edge_pack<BF>((long long)(blockIdx.x - nbot) * 256 + threadIdx.x, K, rn, Bn, ldb, Bs);
+        return;
+    }
     const int cb = blockIdx.x % ncb, r = blockIdx.x / ncb;
     const int c0 = (cb * 256 + (int)threadIdx.x) * 4;
     if (c0 >= N) return;
@@ -187,25 +214,37 @@ __global__ __launch_bounds__(256) void edge_bottom_k(int N, int K, int kr, int n
 }
 
 // C[i][c] = epilogue(sum over ranges r, in order, of P[r][i][c]) for the
-// rm x N bottom edge (C at row m1, rows ldc apart); the loads of 8 ranges are
-// issued before their adds.
+// rm x N bottom edge (C at row m1, rows ldc apart). A workgroup takes 32
+// elements; its 8 thread groups of 32 each add every 8th range (ranges g,
+// g + 8, ... in order), and thread group 0 adds the 8 group sums in group
+// order: a fixed order, with a few loads per thread instead of one per range.
 __global__ __launch_bounds__(256) void edge_reduce_k(float *C, int ldc, const float *P,
                                                      int ranges, int rm, int N, float alpha,
                                                      float beta) {
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    __shared__ float part[8][32];
+    const int t = threadIdx.x, g = t >> 5;
     const long long per = (long long)rm * N;
-    if (e >= per) return;
-    float s = P[e];
-    for (int r0 = 1; r0 < ranges; r0 += 8) {
-        float v[8];
+    const long long e = (long long)blockIdx.x * 32 + (t & 31);
+    float s = 0.0f;
+    if (e < per) {
+        int r = g;
+        float v[4];
+        for (; r + 24 < ranges; r += 32) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = r0 + u < ranges ? P[(size_t)(r0 + u) * per + e] : 0.0f;
+            for (int u = 0; u < 4; ++u) v[u] = P[(size_t)(r + 8 * u) * per + e];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (r0 + u < ranges) s += v[u];
+            for (int u = 0; u < 4; ++u) s += v[u];
+        }
+        for (; r < ranges; r += 8) s += P[(size_t)r * per + e];
     }
+    part[g][t & 31] = s;
+    __syncthreads();
+    if (g != 0 || e >= per) return;
+    float tot = part[0][t];
+#pragma unroll
+    for (int q = 1; q < 8; ++q) tot += part[q][t];
     float *c = C + (size_t)(e / N) * ldc + e % N;
-    *c = bmb::epilogue(s, alpha, beta, c);
+    *c = bmb::epilogue(tot, alpha, beta, c);
 }
 
 // Workgroups of the bottom edge: column blocks of 1024 columns, times K
@@ -237,7 +276,7 @@ static_assert(EDGE_MAX == 8, "with_width covers widths 1 .. 8");
 int bmb::edge_ranges(int N, int K) { return bottom_ranges(N, K); }
 
 long long bmb::edge_partial_floats(int rm, int rn, int N, int K) {
-    return (rm > 0 ? (long long)bottom_ranges(N, K) * rm * N : 0) + (long long)rn * K;
+    return (rm > 0 ? (long long)bottom_ranges(N, K) * rm * N : 0) + 2LL * rn * K;
 }
 
 double bmb::edge_model_s(long long m1, long long rn, long long rm, long long N, long long K) {
@@ -256,38 +295,50 @@ void bmb::gemm_edges(bool bf16x3, int M, int N, int K, int m1, int n1, float alp
     const int rn = N - n1, rm = M - m1;
     const dim3 block(256);
     // P: the bottom edge's partials, then the packed right edge of B.
-    const long long bottom = rm > 0 ? (long long)bottom_ranges(N, K) * rm * N : 0;
-    if (rn > 0 && m1 > 0) {
-        float *Bs = P + bottom;
-        const long long nb = (long long)K * rn;
-        bmb::launch(edge_pack_k, dim3((unsigned)((nb + 255) / 256)), block, 0, stream, K, rn,
-                    B + n1, ldb, Bs);
-        const dim3 grid((unsigned)((m1 + 3) / 4));
-        const float *Bc = Bs;
-        auto right = [&](auto bf, auto rnc) {
-            bmb::launch(edge_right_k<decltype(bf)::value, decltype(rnc)::value>, grid, block, 0,
-                        stream, m1, K, alpha, A, lda, Bc, beta, C + n1, ldc);
-        };
-        with_width(rn, [&](auto rnc) {
-            if (bf16x3) right(std::true_type{}, rnc);
-            else right(std::false_type{}, rnc);
-        });
-    }
+    const int ranges = rm > 0 ? bottom_ranges(N, K) : 0;
+    const long long bottom = (long long)ranges * rm * N;
+    float *Bs = P + bottom;
+    const bool right = rn > 0 && m1 > 0;
+    const int npack = right ? (int)(((long long)K * rn + 255) / 256) : 0;
+    // 1. the bottom edge's partials, with the packing riding the launch
     if (rm > 0) {
-        const int ncb = bottom_ncb(N), ranges = bottom_ranges(N, K);
-        const int kr = (K + ranges - 1) / ranges;
+        const int ncb = bottom_ncb(N);
+        const int kr = (K + ranges - 1) / ranges, nbot = ncb * ranges;
         const float *Am = A + (size_t)m1 * lda;
-        const dim3 grid((unsigned)(ncb * ranges));
+        const dim3 grid((unsigned)(nbot + npack));
         auto bottom_k = [&](auto bf, auto rmc) {
             bmb::launch(edge_bottom_k<decltype(bf)::value, decltype(rmc)::value>, grid, block, 0,
-                        stream, N, K, kr, ncb, Am, lda, B, ldb, P);
+                        stream, N, K, kr, ncb, nbot, Am, lda, B, ldb, P, rn, B + n1, Bs);
         };
         with_width(rm, [&](auto rmc) {
             if (bf16x3) bottom_k(std::true_type{}, rmc);
             else bottom_k(std::false_type{}, rmc);
         });
+    } else if (right) {
+        if (bf16x3)
+            bmb::launch(edge_pack_k<true>, dim3((unsigned)npack), block, 0, stream, K, rn, B + n1,
+                        ldb, Bs);
+        else
+            bmb::launch(edge_pack_k<false>, dim3((unsigned)npack), block, 0, stream, K, rn, B + n1,
+                        ldb, Bs);
+    }
+    // 2. the right edge from the packed B
+    if (right) {
+        const dim3 grid((unsigned)((m1 + 3) / 4));
+        const float *Bc = Bs;
+        auto right_k = [&](auto bf, auto rnc) {
+            bmb::launch(edge_right_k<decltype(bf)::value, decltype(rnc)::value>, grid, block, 0,
+                        stream, m1, K, alpha, A, lda, Bc, beta, C + n1, ldc);
+        };
+        with_width(rn, [&](auto rnc) {
+            if (bf16x3) right_k(std::true_type{}, rnc);
+            else right_k(std::false_type{}, rnc);
+        });
+    }
+    // 3. the bottom edge's reduce and epilogue
+    if (rm > 0) {
         const long long per = (long long)rm * N;
-        bmb::launch(edge_reduce_k, dim3((unsigned)((per + 255) / 256)), block, 0, stream,
+        bmb::launch(edge_reduce_k, dim3((unsigned)((per + 31) / 32)), block, 0, stream,
                     C + (size_t)m1 * ldc, ldc, (const float *)P, ranges, rm, N, alpha, beta);
     }
 }
