@@ -749,12 +749,14 @@ def main():
 
 def sizes_bench(bmb, O, torch):
     """KERNELS ids 8 (fp32 VALU), 9 (fp32 MFMA) and 10 (bf16x3) at N = 512,
-    1024 and 4096 with config 2's epilogue (alpha 1, beta 0.5, C pre-filled),
-    a burst of launches each: the workload of the rocprofv3 counter runs for
-    the VALU and bf16x3 paths and for the small shapes, whose few output
-    tiles leave most CUs idle."""
+    1024, 4096 and 4097 with config 2's epilogue (alpha 1, beta 0.5, C
+    pre-filled), a burst of launches each: the workload of the rocprofv3
+    counter runs for the VALU and bf16x3 paths, for the small shapes, whose
+    few output tiles leave most CUs idle, and for the ragged 4097, which the
+    MFMA paths run as a corner plan (a 4096^2 block of whole tiles, then the
+    edges)."""
     res = {}
-    for n in (512, 1024, 4096):
+    for n in (512, 1024, 4096, 4097):
         dA = torch.from_numpy(O.fill_xorshift(n * n, 0x12345678)).cuda()
         dB = torch.from_numpy(O.fill_xorshift(n * n, 0x9ABCDEF0)).cuda()
         dC = torch.from_numpy(O.fill_xorshift(n * n, 0x0F0F0F0F)).cuda()
