@@ -9,9 +9,10 @@
 // all of their work would be padding; here the VALU streams the large operand
 // once, at HBM rate.
 //  - right: B's K x rn sliver is first packed into rn contiguous rows (for
-//    bf16x3, its split's hi and lo rows), then one wave per row of A, its lanes taking K in float4 steps, rn sums per
-//    lane, a fixed-order butterfly over the wave (every lane ends with the
-//    same bits), and the lanes j < rn store C[row][n1 + j];
+//    bf16x3, its split's hi and lo rows), then one 32-lane half-wave per row
+//    of A, its lanes taking K in float4 steps, rn sums per lane, a
+//    fixed-order butterfly over the half (every lane ends with the same
+//    bits), and the lanes j < rn store C[row][n1 + j];
 //  - bottom: one thread per 4 consecutive columns of B over one of `ranges`
 //    consecutive K ranges, rm x 4 sums per thread, stored as partials
 //    (ranges x rm x N); edge_reduce_k adds them in a fixed order and applies
@@ -94,28 +95,31 @@ __device__ __forceinline__ void load4_tail(const float *p, int i, int n, float (
 }
 
 // Right edge: rows [0, m1), columns [0, RN) of the edge (A at row 0, C at
-// column n1 of row 0; Bs the packed B edge). Four waves per workgroup, one
-// row each; each wave step loads U float4s of the row and of each Bs row
-// before it multiplies, so that many loads per lane are in flight.
+// column n1 of row 0; Bs the packed B edge). Each wave takes two rows, one
+// per 32-lane half, so the two halves' loads of Bs are the same addresses
+// (one fetch) and the packed edge is read once per two rows; four waves per
+// workgroup. Each step loads U float4s of the row and of each Bs row before
+// it multiplies, so that many loads per lane are in flight.
 template <bool BF, int RN>
 __global__ __launch_bounds__(256) void edge_right_k(int m1, int K, float alpha,
                                                     const float *__restrict__ A, int lda,
                                                     const float *__restrict__ Bs, float beta,
                                                     float *C, int ldc) {
     // (BF: Bs holds the split, hi rows then lo rows; twice the B loads per step.)
-    constexpr int U = (BF ? 2 : 1) * RN <= 2 ? 8 : (BF ? 2 : 1) * RN <= 4 ? 4 : 2;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= m1) return;  // (uniform over the wave)
+    constexpr int NB = BF ? 2 : 1;  // B rows per column: the value, or its hi and lo
+    constexpr int U = NB * RN <= 2 ? 8 : NB * RN <= 4 ? 4 : 2;
+    const int lane = threadIdx.x & 63, l32 = lane & 31;
+    const int row = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * 2 + (lane >> 5);
+    if (row - (lane >> 5) >= m1) return;  // both rows past the end (uniform over the wave)
     float acc[RN];
 #pragma unroll
     for (int j = 0; j < RN; ++j) acc[j] = 0.0f;
-    const float *a = A + (size_t)row * lda;
-    constexpr int NB = BF ? 2 : 1;  // B rows per column: the value, or its hi and lo
-    for (int k0 = lane * 4; k0 < K; k0 += 256 * U) {
+    const float *a = A + (size_t)min(row, m1 - 1) * lda;  // (a row past the end stores nothing)
+    for (int k0 = l32 * 4; k0 < K; k0 += 128 * U) {
         float av[U][4], bv[U][NB * RN][4];
 #pragma unroll
         for (int s = 0; s < U; ++s) {
-            const int k = k0 + 256 * s;
+            const int k = k0 + 128 * s;
             load4_tail(a, k, K, av[s]);
 #pragma unroll
             for (int j = 0; j < NB * RN; ++j) load4_tail(Bs + (size_t)j * K, k, K, bv[s][j]);
@@ -139,11 +143,11 @@ __global__ __launch_bounds__(256) void edge_right_k(int m1, int K, float alpha,
     for (int j = 0; j < RN; ++j) {
         float v = acc[j];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == j) out = v;
+        for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off);  // within the half
+        if (l32 == j) out = v;
     }
-    if (lane < RN) {
-        float *c = C + (size_t)row * ldc + lane;
+    if (l32 < RN && row < m1) {
+        float *c = C + (size_t)row * ldc + l32;
         *c = bmb::epilogue(out, alpha, beta, c);
     }
 }
@@ -324,7 +328,7 @@ void bmb::gemm_edges(bool bf16x3, int M, int N, int K, int m1, int n1, float alp
     }
     // 2. the right edge from the packed B
     if (right) {
-        const dim3 grid((unsigned)((m1 + 3) / 4));
+        const dim3 grid((unsigned)((m1 + 7) / 8));
         const float *Bc = Bs;
         auto right_k = [&](auto bf, auto rnc) {
             bmb::launch(edge_right_k<decltype(bf)::value, decltype(rnc)::value>, grid, block, 0,
