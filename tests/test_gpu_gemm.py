@@ -515,3 +515,47 @@ def test_corner_edges(gpu, shape, math, capfd, monkeypatch):
     n1 = N // 256 * 256
     e_edge, bad = O.normwise(got[rows][:, n1:], ref[:, n1:])
     assert bad == 0 and e_edge < (fp32_order_bound(3 * K) if math == 0 else fp32_order_bound(K))
+
+
+@pytest.mark.parametrize("math", [0, 1], ids=["bf16x3", "fp32"])
+@pytest.mark.parametrize("rm,rn", [(2, 3), (6, 8), (8, 1), (3, 0), (0, 6)],
+                         ids=lambda v: str(v))
+def test_corner_edge_widths(gpu, rm, rn, math, capfd, monkeypatch):
+    """Edge widths 0-8 on a block of whole tiles (K = 4096; the bf16x3
+    planner takes the corner plan from a 4096^2 block, the fp32 one already
+    from 2048^2): every edge row and column against fp64, the edges' own
+    bound, and the plan trace showing the edge kernels ran."""
+    base = 4096 if math == 0 else 2048
+    M, N, K = base + rm, base + rn, 4096
+    A = O.fill_xorshift(M * K, 0x1357)
+    B = O.fill_xorshift(K * N, 0x2468)
+    C0 = O.fill_xorshift(M * N, 0x3579)
+    monkeypatch.setenv("BMB_GEMM_PLAN_TRACE", "1")
+    with bmb.gemm_math(math):
+        dA, dB, dC = dev(A), dev(B), dev(C0)
+        print("gemm NN %dx%dx%d math %d" % (M, N, K, math), flush=True)
+        bmb.gemm(False, False, M, N, K, 0.5, dA.data_ptr(), dB.data_ptr(), 2.0, dC.data_ptr())
+        sync("gemm corner edge widths")
+    err_out = capfd.readouterr().err
+    plan = [l for l in err_out.splitlines() if "gemm plan %dx%dx%d:" % (M, N, K) in l]
+    assert plan and "edges 1" in plan[0], err_out
+    got = dC.cpu().numpy().reshape(M, N)
+    rows = np.unique(np.r_[0, 1, 511, 512, 1023, base - 1, np.arange(base, M)])
+    ref = O.gemm_f64(False, False, len(rows), N, K, 0.5, A.reshape(M, K)[rows], B, 2.0,
+                     C0.reshape(M, N)[rows])
+    bound = fp32_order_bound(3 * K) if math == 0 else fp32_order_bound(K)
+    err, bad = O.normwise(got[rows], ref)
+    assert bad == 0 and err < 1e-4
+    if math == 0:
+        e3, b3 = bf16x3_err(got[rows], False, False, len(rows), N, K, 0.5,
+                            A.reshape(M, K)[rows], B, 2.0, C0.reshape(M, N)[rows])
+        assert e3 < b3, (e3, b3)
+    else:
+        assert err < bound, err
+    if rn:
+        # the right edge over every row
+        refc = O.gemm_f64(False, False, M, rn, K, 0.5, A.reshape(M, K),
+                          np.ascontiguousarray(B.reshape(K, N)[:, base:]), 2.0,
+                          np.ascontiguousarray(C0.reshape(M, N)[:, base:]))
+        ec, bad = O.normwise(got[:, base:], refc)
+        assert bad == 0 and ec < bound, ec
