@@ -32,6 +32,7 @@ using TileL = MfmaTile<256, 256, 32, 2, 4>;  // 512 lanes, 128x64 per wave, K de
 using TileM = MfmaTile<128, 128, 16, 2, 2>;  // 256 lanes, 64x64 per wave
 using TileN = MfmaTile<64, 128, 16, 2, 2>;   // 256 lanes, 32x64 per wave
 using TileS = MfmaTile<64, 64, 16, 2, 2>;    // 256 lanes, 32x32 per wave
+using TileXS = MfmaTile<32, 32, 16, 1, 1>;   // 64 lanes (k-sliced only: 4 or 8 slices)
 
 // Number of CUs of the current device (256 on MI355X), cached per device.
 int device_cus() {
@@ -71,8 +72,11 @@ int device_cus() {
 // partials in global memory and no reduce launch): for few output tiles it
 // puts more waves on each SIMD without split-K's round trip. Those kernels
 // exist for the plain BLAS epilogue only (KERNELS id 9, gemm() in fp32 mode,
-// batched_gemm()).
-enum class TileKind { L, M, N, S };
+// batched_gemm()). The 32 x 32 tile exists only k-sliced (one wave per
+// slice), for problems too small to give every CU a 64 x 64 tile (N = 512:
+// 64 of them, or 256 split-K items plus a reduce launch), and is only
+// considered up to XS_MAX_OUTPUTS outputs.
+enum class TileKind { L, M, N, S, XS };
 struct Cand {
     TileKind kind;
     int bm, bn;
@@ -87,8 +91,11 @@ constexpr Cand CANDS[] = {{TileKind::L, 256, 256, 0.909, 1},
                           {TileKind::N, 64, 128, 0.823, 2},
                           {TileKind::N, 64, 128, 0.823, 4},
                           {TileKind::S, 64, 64, 0.809, 2},
-                          {TileKind::S, 64, 64, 0.809, 4}};
+                          {TileKind::S, 64, 64, 0.809, 4},
+                          {TileKind::XS, 32, 32, 0.5, 4},
+                          {TileKind::XS, 32, 32, 0.5, 8}};
 constexpr int N_CANDS = sizeof(CANDS) / sizeof(CANDS[0]);
+constexpr long long XS_MAX_OUTPUTS = 1LL << 20;
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 constexpr double K_OVERHEAD = 60.0;           // per-item prologue/epilogue, in k steps
 constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last round
@@ -242,6 +249,7 @@ double best_part(int M, int N, int K, int batch, bool may_split, const Occupancy
         const Cand &c = CANDS[ci];
         if (occ.wgs[ci][0] <= 0) continue;  // no such kernel for this case
         if (c.ks > 1 && K < c.ks * MIN_SLICE_K) continue;
+        if (c.kind == TileKind::XS && (long long)M * N * batch > XS_MAX_OUTPUTS) continue;
         for (int s : SPLITS) {
             int splits = 1, kchunk = round_up16(K);
             if (s > 1) {
@@ -385,6 +393,8 @@ const Occupancy &occupancy(bool vec) {
             ks_occupancy<TA, TB, TileN, EPI, true, 4>(o.wgs[6]);
             ks_occupancy<TA, TB, TileS, EPI, true, 2>(o.wgs[7]);
             ks_occupancy<TA, TB, TileS, EPI, true, 4>(o.wgs[8]);
+            ks_occupancy<TA, TB, TileXS, EPI, true, 4>(o.wgs[9]);
+            ks_occupancy<TA, TB, TileXS, EPI, true, 8>(o.wgs[10]);
         } else {
             tile_occupancy<TA, TB, TileL, EPI, false>(o.wgs[0]);
             tile_occupancy<TA, TB, TileM, EPI, false>(o.wgs[1]);
@@ -395,6 +405,8 @@ const Occupancy &occupancy(bool vec) {
             ks_occupancy<TA, TB, TileN, EPI, false, 4>(o.wgs[6]);
             ks_occupancy<TA, TB, TileS, EPI, false, 2>(o.wgs[7]);
             ks_occupancy<TA, TB, TileS, EPI, false, 4>(o.wgs[8]);
+            ks_occupancy<TA, TB, TileXS, EPI, false, 4>(o.wgs[9]);
+            ks_occupancy<TA, TB, TileXS, EPI, false, 8>(o.wgs[10]);
         }
     });
     return table[dev][vec];
@@ -491,6 +503,7 @@ void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const 
         case TileKind::M: launch_split<TA, TB, TileM, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
         case TileKind::N: launch_split<TA, TB, TileN, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
         case TileKind::S: launch_split<TA, TB, TileS, EPI>(p, M, N, K, alpha, o, beta, P, vec, ep, stream); break;
+        case TileKind::XS: break;  // (never split: k-sliced only)
         }
         return;
     }
@@ -504,6 +517,10 @@ void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const 
             if (ks == 2) launch_tile_ks<TA, TB, TileN, EPI, 2>(batch, M, N, K, alpha, o, beta, stream, vec);
             else launch_tile_ks<TA, TB, TileN, EPI, 4>(batch, M, N, K, alpha, o, beta, stream, vec);
             break;
+        case TileKind::XS:
+            if (ks == 4) launch_tile_ks<TA, TB, TileXS, EPI, 4>(batch, M, N, K, alpha, o, beta, stream, vec);
+            else launch_tile_ks<TA, TB, TileXS, EPI, 8>(batch, M, N, K, alpha, o, beta, stream, vec);
+            break;
         default:
             if (ks == 2) launch_tile_ks<TA, TB, TileS, EPI, 2>(batch, M, N, K, alpha, o, beta, stream, vec);
             else launch_tile_ks<TA, TB, TileS, EPI, 4>(batch, M, N, K, alpha, o, beta, stream, vec);
@@ -516,6 +533,7 @@ void run_band(const Part &p, int batch, int M, int N, int K, float alpha, const 
     case TileKind::M: launch_tile<TA, TB, TileM, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
     case TileKind::N: launch_tile<TA, TB, TileN, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
     case TileKind::S: launch_tile<TA, TB, TileS, EPI>(batch, M, N, K, alpha, o, beta, stream, vec, ep); break;
+    case TileKind::XS: break;  // (k-sliced only, above)
     }
 }
 
