@@ -75,7 +75,14 @@ int device_cus() {
 // batched_gemm()). The 32 x 32 tile exists only k-sliced (one wave per
 // slice), for problems too small to give every CU a 64 x 64 tile (N = 512:
 // 64 of them, or 256 split-K items plus a reduce launch), and is only
-// considered up to XS_MAX_OUTPUTS outputs.
+// considered up to XS_MAX_OUTPUTS outputs. Each slice beyond the first adds
+// KS_OVERHEAD k steps to its workgroup's item (its own prologue, and the sum
+// of the slices in LDS): without that charge the model put the GPT-2 forward
+// and dX products with K = 768 (8192 x 2304 and 8192 x 768, thousands of
+// tiles) on 4-sliced 64 x 128 tiles, 11-14% slower than the plain 64 x 128
+// tile, while a forced sweep of every plan (23 shapes, 1000 plans) puts the
+// charge anywhere in 16-28 k steps with the measured best plan picked on 21
+// of them and the other two within 1.3%.
 enum class TileKind { L, M, N, S, XS };
 struct Cand {
     TileKind kind;
@@ -98,6 +105,7 @@ constexpr int N_CANDS = sizeof(CANDS) / sizeof(CANDS[0]);
 constexpr long long XS_MAX_OUTPUTS = 1LL << 20;
 constexpr int SPLITS[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 constexpr double K_OVERHEAD = 60.0;           // per-item prologue/epilogue, in k steps
+constexpr double KS_OVERHEAD = 24.0;          // per k-slice beyond the first, in k steps
 constexpr double PARTIAL_EXP = 0.88;          // speed of a part-filled last round
 constexpr double PARTIALS_BYTES_PER_S = 1.35e13;  // the partials' round trip
 constexpr double LAUNCH_S = 1.6e-6;           // the reduce launch
@@ -224,7 +232,8 @@ double model_time(long long M, long long N, long long K, long long batch, const 
     const long long items = tiles * splits;
     const long long slots = (long long)cus * occ;
     const double peak_cu = 157.3e12 / 256.0;
-    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) / (c.eff * peak_cu) * occ;
+    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD + (c.ks - 1) * KS_OVERHEAD) /
+                          (c.eff * peak_cu) * occ;
     // (a k-sliced workgroup: occ counts workgroups of ks slices each)
     const long long full = items / slots, rem = items % slots;
     double t = full * t_item;
