@@ -9,11 +9,14 @@ namespace bmb {
 struct ScratchBuffer {
     void *ptr = nullptr;
     size_t cap = 0;
-    // Recorded on the last lessee's stream when it returned the buffer;
-    // `recorded` is false until the first return.
+    // Completes after the last lessee's work: recorded on its stream when it
+    // returned the buffer (a created stream), or, for a lessee on the null
+    // stream, only when a lease on another stream takes the buffer (`on_null`:
+    // the last lessee used the null stream and `done` is not recorded yet).
     hipEvent_t done = nullptr;
     bool recorded = false;
-    hipStream_t last = nullptr;  // the stream `done` was last recorded on
+    bool on_null = false;
+    hipStream_t last = nullptr;  // the last lessee's stream
 };
 
 namespace {
@@ -64,13 +67,30 @@ ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes, hipStream_t stream)
         }
     }
     dev_ = dev;
+    // The event only orders device work on one device (a later lessee's
+    // kernels after an earlier one's), so it needs no system-scope fence: a
+    // fenced event costs about 3 us of device time per record, one without it
+    // about 1.5.
     if (buf_->done == nullptr &&
-        hipEventCreateWithFlags(&buf_->done, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&buf_->done, hipEventDisableTiming | hipEventDisableSystemFence) !=
+            hipSuccess) {
         (void)hipGetLastError();
         buf_->done = nullptr;
         return;  // no way to order reuse: no buffer (the destructor puts it back)
     }
-    if (buf_->cap < bytes) {
+    const bool grow = buf_->cap < bytes;
+    if (buf_->on_null && (grow || stream_ != nullptr)) {
+        // The last lessee's work is on the null stream, queued before
+        // anything queued there from now on: an event recorded there now
+        // completes after it.
+        if (hipEventRecord(buf_->done, nullptr) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        buf_->recorded = true;
+        buf_->on_null = false;
+    }
+    if (grow) {
         if (buf_->ptr != nullptr) {
             // Work queued by an earlier lessee may still read the old buffer.
             if (buf_->recorded && hipEventSynchronize(buf_->done) != hipSuccess) {
@@ -92,15 +112,26 @@ ScratchLease::ScratchLease(ScratchSlot slot, size_t bytes, hipStream_t stream)
         (void)hipGetLastError();
         return;
     }
+    // (on_null left set: this lessee is on the null stream too, where its
+    // work runs after the last lessee's in queue order.)
     ptr_ = buf_->ptr;
 }
 
 ScratchLease::~ScratchLease() {
     if (buf_ == nullptr) return;
-    if (ptr_ != nullptr) {
-        // After everything this lease's caller queued on its stream.
+    if (ptr_ != nullptr && stream_ == nullptr) {
+        // The null stream is never destroyed: the event is recorded there only
+        // when a lease on another stream takes the buffer (one record per call
+        // saved for the common case of back-to-back calls on the null stream).
+        buf_->on_null = true;
+        buf_->recorded = false;
+        buf_->last = nullptr;
+    } else if (ptr_ != nullptr) {
+        // After everything this lease's caller queued on its stream (recorded
+        // now: the caller may destroy its stream).
         if (hipEventRecord(buf_->done, stream_) == hipSuccess) {
             buf_->recorded = true;
+            buf_->on_null = false;
             buf_->last = stream_;
         } else {
             (void)hipGetLastError();

@@ -17,8 +17,12 @@
 // call has queued its work, so reuse is ordered on the device by an event:
 // the lease's destructor records the buffer's event on the lessee's stream
 // (after every kernel the call queued there), and the next lease makes its
-// own stream wait for that event before anything it queues. Two calls on
-// different streams, or on the null stream from several host threads,
+// own stream wait for that event before anything it queues. A lessee on the
+// null stream records nothing when it returns the buffer: a next lease on
+// the null stream queues after its work anyway, and a next lease on another
+// stream records the event on the null stream then (after everything queued
+// there so far, the last lessee's work included) and waits for it. Two calls
+// on different streams, or on the null stream from several host threads,
 // therefore never touch one buffer at the same time. A lease prefers an idle
 // buffer last used on its own stream, so that work on two streams does not
 // wait on each other through the pool. A buffer that must grow is freed only

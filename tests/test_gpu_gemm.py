@@ -317,6 +317,44 @@ def test_two_streams_share_scratch_in_order(gpu):
             assert np.array_equal(o.cpu().numpy().view(np.uint32), d["ref"])
 
 
+def test_null_and_side_stream_share_scratch_in_order(gpu):
+    """A lease on the null stream records no event when it returns its
+    buffer; a lease on another stream that takes the buffer records one on
+    the null stream then and waits for it. Split-K gemm() calls alternate
+    between the null stream and a side stream (torch's pool streams do not
+    synchronise with the null stream), with no host synchronisation, a large
+    shape on the null stream each time so that its reduce is still running
+    when the side stream's call is queued. Every result equals its bits from
+    calls made one at a time."""
+    import torch
+    shapes = [(3072, 768, 8192, True), (768, 768, 8192, True)]
+    data = []
+    for i, (M, N, K, ta) in enumerate(shapes):
+        A = O.fill_xorshift(M * K, 0x5150 + i)
+        B = O.fill_xorshift(K * N, 0x6160 + i)
+        d = {"A": dev(A), "B": dev(B), "shape": (M, N, K, ta)}
+        d["C"] = torch.empty(M * N, device="cuda", dtype=torch.float32)
+        bmb.gemm(ta, False, M, N, K, 1.0, d["A"].data_ptr(), d["B"].data_ptr(), 0.0,
+                 d["C"].data_ptr())
+        sync("reference gemm")
+        d["ref"] = d["C"].cpu().numpy().view(np.uint32).copy()
+        d["outs"] = [torch.empty(M * N, device="cuda", dtype=torch.float32) for _ in range(4)]
+        data.append(d)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    print("null stream and side stream x 4 split-K gemm() calls", flush=True)
+    for r in range(4):
+        for d, s in zip(data, (0, side.cuda_stream)):
+            M, N, K, ta = d["shape"]
+            bmb.gemm(ta, False, M, N, K, 1.0, d["A"].data_ptr(), d["B"].data_ptr(), 0.0,
+                     d["outs"][r].data_ptr(), s)
+    torch.cuda.synchronize()
+    bmb.check("gemm on the null and a side stream")
+    for d in data:
+        for o in d["outs"]:
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), d["ref"])
+
+
 # ---- gemm_set_math(GEMM_MATH_FP32): fp32 matrix-core products, held to the
 # fp32 summation bound (the rounding level of the reference's fp32 gemm()).
 
