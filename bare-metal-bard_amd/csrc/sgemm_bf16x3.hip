@@ -641,12 +641,17 @@ constexpr double LAUNCH_S = 1.6e-6;               // the reduce launch
 // tried for K >= MIN_BAND_K, with K ranges of at least MIN_BAND_SPLIT_K in a
 // split remainder band, and taken when modelled 3% faster than one band:
 // measured on MI355X, bands gained 15-18% at N = 4097 and 6144 and on the
-// GPT-2 LM-head weight gradient (K = 8192) and lost 3-7% on the K = 768 and
-// 3072 GPT-2 GEMMs of about 100 us, whose short K ranges the model
-// undercharges.
+// GPT-2 LM-head weight gradient (K = 8192), and 4.5% on the GPT-2 QKV
+// forward (8192 x 2304 x 768: 7168 rows on 256 x 256 tiles in two whole
+// rounds, the last 1024 on 128 x 128). Without the bound on the remainder's
+// K ranges they lost 3-7% on the K = 768 and 3072 GPT-2 GEMMs, whose short
+// split ranges the model undercharges; with it, no other GPT-2 or square
+// sweep shape changes plan. Corner plans (below) are tried for
+// K >= MIN_CORNER_K only, the range they were measured on.
 constexpr double BAND_S = 12.0e-6;
 constexpr double BAND_GAIN = 0.97;
-constexpr int MIN_BAND_K = 4096;
+constexpr int MIN_BAND_K = 768;
+constexpr int MIN_CORNER_K = 4096;
 constexpr int MIN_BAND_SPLIT_K = 512;
 constexpr int MIN_SPLIT_K = 64;  // two stages
 constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;  // 256 MiB of partials
@@ -791,7 +796,7 @@ Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats
     // Corner plans: whole tiles of one candidate over [0, m1) x [0, n1), the
     // edges on the edge kernels (row-major A and B, BLAS epilogue; their
     // scratch only where K may be split).
-    for (int t = 0; edges_ok && may_split && K >= MIN_BAND_K && t < N_CANDS; ++t) {
+    for (int t = 0; edges_ok && may_split && K >= MIN_CORNER_K && t < N_CANDS; ++t) {
         const B3Cand &c = CANDS[t];
         const int m1 = M / c.bm * c.bm, n1 = N / c.bn * c.bn;
         if (m1 == 0 || n1 == 0 || (m1 == M && n1 == N) || M - m1 > bmb::EDGE_MAX ||
