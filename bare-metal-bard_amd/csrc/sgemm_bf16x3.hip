@@ -94,6 +94,7 @@ using TileL = B3Tile<256, 256, 2, 4>;
 using TileM = B3Tile<128, 128, 2, 2>;
 using TileS = B3Tile<64, 64, 2, 2>;
 using TileT = B3Tile<128, 256, 2, 4>;
+using TileXS = B3Tile<32, 32, 1, 1>;  // one wave (k-sliced kernels only)
 
 // Offset (in bf16) of element k (a multiple of 4) of LDS row `row`. Rows are
 // 64 bytes (four 16-byte chunks); row r is stored in slot p = r ^ ((r >> 2)
@@ -425,13 +426,19 @@ struct Bf16x3Gemm {
     // are guarded (zero fill past K); every other stage runs the interior
     // loop. EPI: what the epilogue stores (bmb::Epi; EPI_PARTIAL: the raw
     // sums). C's rows (and those of ep.act, ep.pre) are ldc floats apart.
-    template <bool INTERIOR, int EPI, bool KTAIL = false>
+    // KS > 1: the workgroup is KS k-slices of NT lanes (bf16x3_ks_k); this
+    // slice's stages are at smem, K is its range's length (<= 0: none of its
+    // stages holds data) and every slice runs kloop stages, so that all of
+    // them meet at the same barriers. The slices' sums are then added in LDS,
+    // in slice order, and slice 0 runs the epilogue.
+    template <bool INTERIOR, int EPI, bool KTAIL = false, int KS = 1>
     __device__ static __forceinline__ void run(int M, int N, int K, int lda, int ldb, float alpha,
                                                const float *__restrict__ A,
                                                const float *__restrict__ B, float beta, float *C,
                                                int ldc, int m0, int n0, __bf16 *smem,
-                                               const bmb::EpiArgs &ep) {
-        const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+                                               const bmb::EpiArgs &ep, int kloop = 0) {
+        const int tid = KS > 1 ? (int)(threadIdx.x % NT) : (int)threadIdx.x;
+        const int wave = tid >> 6, lane = tid & 63;
         const int wm = (wave / Tl::WAVES_N) * Tl::WM, wn = (wave % Tl::WAVES_N) * Tl::WN;
 
         f32x16 acc[FM][FN];
@@ -442,7 +449,7 @@ struct Bf16x3Gemm {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[fi][fn][r] = 0.0f;
 
-        const int nkt = (K + BK - 1) / BK;
+        const int nkt = KS > 1 ? kloop : (K + BK - 1) / BK;
         SA ga;
         SB gb;
         unsigned oa[SA::NLD], ob[SB::NLD];
@@ -498,6 +505,39 @@ struct Bf16x3Gemm {
             }
             step(st, 1, wm, wn, lane, acc);
             __syncthreads();
+        }
+
+        if constexpr (KS > 1) {
+            // Slices 1 .. KS-1 leave their sums in LDS (over the stages, which
+            // every slice has finished reading at the loop's last barrier);
+            // slice 0 adds them in slice order.
+            const int slice = (int)(threadIdx.x / NT);
+            float *red = reinterpret_cast<float *>(smem - (size_t)slice * 2 * Tl::STAGE);
+            static_assert((size_t)(KS - 1) * FM * FN * 16 * NT * sizeof(float) <=
+                              (size_t)KS * Tl::SMEM_BYTES,
+                          "the slices' sums fit in the workgroup's stages");
+            if (slice > 0) {
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            red[((((size_t)slice - 1) * FM + fi) * FN + fn) * 16 * NT + r * NT + tid] =
+                                acc[fi][fn][r];
+            }
+            __syncthreads();
+            if (slice > 0) return;
+#pragma unroll 1
+            for (int sl = 1; sl < KS; ++sl)
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[fi][fn][r] +=
+                                red[((((size_t)sl - 1) * FM + fi) * FN + fn) * 16 * NT + r * NT + tid];
         }
 
         // Epilogue: lanes 0-31 of a register cover 32 consecutive columns.
@@ -594,6 +634,40 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
                                     lds, ep);
 }
 
+// The same tile as KS k-slices of Tl::NT lanes each (any epilogue but a
+// split-K partial: it never splits): slice s takes k-stages [s per, (s + 1) per) of the per = ceil(
+// stages / KS) each slice runs, its stages in its own KS-th of the LDS, and
+// the slices' sums meet in LDS (Bf16x3Gemm::run). For problems with too few
+// output tiles to fill the device, where split-K would need a second launch
+// for its reduce. Interior tiles take the unguarded loop when every slice's
+// range is whole stages (K a multiple of KS * BK).
+template <class Tl, bool TA, bool TB, bool VEC, int EPI, int KS>
+__global__ __launch_bounds__(Tl::NT * KS) void bf16x3_ks_k(int M, int N, int K, float alpha,
+                                                           const float *__restrict__ A, int lda,
+                                                           const float *__restrict__ B, int ldb,
+                                                           float beta, float *C, int ldc,
+                                                           int tiles_m, int tiles_n,
+                                                           bmb::EpiArgs ep) {
+    extern __shared__ __bf16 lds[];
+    using G = Bf16x3Gemm<Tl, TA, TB, VEC>;
+    int tm, tn;
+    bmb::group_tile(bmb::xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * Tl::BM, n0 = tn * Tl::BN;
+    const int slice = (int)(threadIdx.x / Tl::NT);
+    const int per = ((K + BK - 1) / BK + KS - 1) / KS;
+    const int kb = slice * per * BK;
+    const int klen = min(K - kb, per * BK);  // <= 0: a slice past K (zero stages of data)
+    const float *Ak = TA ? A + (size_t)min(kb, K) * lda : A + min(kb, K);
+    const float *Bk = TB ? B + min(kb, K) : B + (size_t)min(kb, K) * ldb;
+    __bf16 *st = lds + (size_t)slice * 2 * Tl::STAGE;
+    if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && K > 0 && K % (KS * BK) == 0)
+        G::template run<true, EPI, false, KS>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, C, ldc,
+                                              m0, n0, st, ep, per);
+    else
+        G::template run<false, EPI, false, KS>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, C, ldc,
+                                               m0, n0, st, ep, per);
+}
+
 // ------------------------------------------------------------- host side
 
 // Tile and split choice, the fp32 MFMA planner's time model (mfma_gemm.hip)
@@ -621,9 +695,24 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 struct B3Cand {
     int bm, bn;
     double tflops;  // fitted fp32-equivalent TFLOP/s when the device is full of them
+    int ks;         // k-slices per workgroup (bf16x3_ks_k; never split)
 };
-constexpr B3Cand CANDS[] = {{256, 256, 452.0}, {128, 128, 326.0}, {64, 64, 233.0}, {128, 256, 345.0}};
-constexpr int N_CANDS = 4;
+constexpr B3Cand CANDS[] = {{256, 256, 452.0, 1}, {128, 128, 326.0, 1}, {64, 64, 233.0, 1},
+                            {128, 256, 345.0, 1}, {64, 64, 233.0, 2},  {64, 64, 233.0, 4},
+                            {32, 32, 180.0, 4},   {32, 32, 180.0, 8}};
+constexpr int N_CANDS = 8;
+// A k-sliced workgroup: each slice beyond the first adds KS_OVERHEAD k to its
+// item (its own prologue and the slices' sum in LDS); the 32 x 32 tile only
+// for problems of at most XS_MAX_OUTPUTS outputs, every slice at least
+// MIN_SLICE_K of k. Fitted to a forced sweep of every plan on ten problems
+// of 0.06-1.1 M outputs (the squares 512-2048, 256 x 256 x 4096, 512 x 512
+// x 2048, 384 x 384 x 1000, 128 x 1024 x 8192): the model's plan is the
+// measured best on all but N = 2048 (5%, as before). The k-sliced plans
+// replace split-K plus its reduce at N = 512 (9.5 -> 5.6 us), 768, 1000 and
+// 1024 (19.4 -> 15.0 us); no GPT-2 shape or square above 1024 changes plan.
+constexpr double KS_OVERHEAD = 64.0;
+constexpr long long XS_MAX_OUTPUTS = 1LL << 20;
+constexpr int MIN_SLICE_K = 64;
 // Split counts that are not powers of two fill the device in one round where
 // {2, 4, 8} do not (the GPT-2 weight gradients: 36 tiles of 256 x 256 in 7
 // ranges on 256 CUs, 36 of 128 x 128 in 14 on 512 slots: 18-36% faster). The
@@ -656,17 +745,24 @@ constexpr int MIN_BAND_SPLIT_K = 512;
 constexpr int MIN_SPLIT_K = 64;  // two stages
 constexpr long long MAX_SPLIT_FLOATS = 64LL << 20;  // 256 MiB of partials
 
-template <class Tl>
-int occupancy_of() {
+template <class Kern>
+int occupancy_of(Kern kern, int threads, size_t smem) {
     int n = 0;
-    auto kern = bf16x3_k<Tl, false, false, true, bmb::EPI_BLAS>;
-    bmb::allow_smem(kern, Tl::SMEM_BYTES);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, Tl::NT, Tl::SMEM_BYTES) !=
-        hipSuccess) {
+    bmb::allow_smem(kern, smem);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, smem) != hipSuccess) {
         (void)hipGetLastError();
         n = 1;
     }
     return n < 1 ? 1 : n;
+}
+template <class Tl>
+int occupancy_of() {
+    return occupancy_of(bf16x3_k<Tl, false, false, true, bmb::EPI_BLAS>, Tl::NT, Tl::SMEM_BYTES);
+}
+template <class Tl, int KS>
+int ks_occupancy_of() {
+    return occupancy_of(bf16x3_ks_k<Tl, false, false, true, bmb::EPI_BLAS, KS>, Tl::NT * KS,
+                        KS * Tl::SMEM_BYTES);
 }
 
 // One band's launch: tile candidate, K ranges and the K per range.
@@ -700,6 +796,10 @@ const Device &device_info(int dev) {
         d.occ[1] = occupancy_of<TileM>();
         d.occ[2] = occupancy_of<TileS>();
         d.occ[3] = occupancy_of<TileT>();
+        d.occ[4] = ks_occupancy_of<TileS, 2>();
+        d.occ[5] = ks_occupancy_of<TileS, 4>();
+        d.occ[6] = ks_occupancy_of<TileXS, 4>();
+        d.occ[7] = ks_occupancy_of<TileXS, 8>();
         int c = 0;
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             c <= 0) {
@@ -717,6 +817,10 @@ bool part_time(const Device &dv, int M, int N, int K, int t, int s, bool may_spl
                long long max_floats, Part &out, double &time) {
     const B3Cand &c = CANDS[t];
     int splits = 1, kchunk = K;
+    if (c.ks > 1) {
+        if (s > 1 || K < c.ks * MIN_SLICE_K) return false;
+        if (c.bm == 32 && (long long)M * N > XS_MAX_OUTPUTS) return false;
+    }
     if (s > 1) {
         if (!may_split || K < 2 * MIN_SPLIT_K) return false;
         kchunk = (K + s - 1) / s;
@@ -730,8 +834,8 @@ bool part_time(const Device &dv, int M, int N, int K, int t, int s, bool may_spl
     const long long items = tiles * splits;
     const int occ = dv.occ[t], cus = dv.cus;
     const long long slots = (long long)cus * occ;
-    const double t_item =
-        2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD) * occ / (c.tflops * 1e12 / cus);
+    const double t_item = 2.0 * c.bm * c.bn * (kchunk + K_OVERHEAD + (c.ks - 1) * KS_OVERHEAD) *
+                          occ / (c.tflops * 1e12 / cus);
     const long long full = items / slots, rem = items % slots;
     time = full * t_item;
     if (rem) {
@@ -747,13 +851,14 @@ bool part_time(const Device &dv, int M, int N, int K, int t, int s, bool may_spl
 }
 
 // The fastest single-band plan of an M x N x K band (split K ranges of at
-// least min_split_k).
+// least min_split_k; k-sliced tiles only if ks_ok).
 double best_part(const Device &dv, int M, int N, int K, bool may_split, long long max_floats,
-                 Part &best, int min_split_k = 0) {
+                 Part &best, int min_split_k = 0, bool ks_ok = false) {
     double best_t = -1.0;
     best = Part{0, 1, K};
     for (int t = 0; t < N_CANDS; ++t)
         for (int s : SPLITS) {
+            if (CANDS[t].ks > 1 && !ks_ok) continue;
             Part p;
             double tm;
             if (part_time(dv, M, N, K, t, s, may_split, max_floats, p, tm) &&
@@ -765,15 +870,18 @@ double best_part(const Device &dv, int M, int N, int K, bool may_split, long lon
     return best_t;
 }
 
+// ks_ok: the k-sliced tiles may run the problem (single-band plans only).
 Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats,
-              bool edges_ok) {
+              bool edges_ok, bool ks_ok) {
     const Device &dv = device_info(dev);
     Plan best{{Part{0, 1, K}, Part{0, 1, K}}, M, N, false};
-    const double single_t = best_part(dv, M, N, K, may_split, max_floats, best.part[0]);
+    const double single_t =
+        best_part(dv, M, N, K, may_split, max_floats, best.part[0], 0, ks_ok);
     double best_t = single_t;
     // Two bands: the first whole rounds of one tile, the rest on its own plan.
     for (int t = 0; K >= MIN_BAND_K && t < N_CANDS; ++t) {
         const B3Cand &c = CANDS[t];
+        if (c.ks > 1) continue;
         const long long tiles_n = bmb::ceil_div(N, c.bn);
         const long long slots = (long long)dv.cus * dv.occ[t];
         for (long long k = 1;; ++k) {
@@ -798,6 +906,7 @@ Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats
     // scratch only where K may be split).
     for (int t = 0; edges_ok && may_split && K >= MIN_CORNER_K && t < N_CANDS; ++t) {
         const B3Cand &c = CANDS[t];
+        if (c.ks > 1) continue;
         const int m1 = M / c.bm * c.bm, n1 = N / c.bn * c.bn;
         if (m1 == 0 || n1 == 0 || (m1 == M && n1 == N) || M - m1 > bmb::EDGE_MAX ||
             N - n1 > bmb::EDGE_MAX || bmb::edge_partial_floats(M - m1, N - n1, N, K) > max_floats)
@@ -823,19 +932,20 @@ Plan plan_for(int dev, int M, int N, int K, bool may_split, long long max_floats
 // Plans are memoised per (device, shape, split permission and cap): the
 // search above costs tens of microseconds, a GEMM call in a training step
 // a few hundred.
-Plan pick(int M, int N, int K, bool may_split, long long max_floats, bool edges_ok) {
+Plan pick(int M, int N, int K, bool may_split, long long max_floats, bool edges_ok,
+          bool ks_ok) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    using Key = std::tuple<int, int, int, int, bool, long long, bool>;
+    using Key = std::tuple<int, int, int, int, bool, long long, bool, bool>;
     static std::mutex mu;
     static std::map<Key, Plan> memo;
-    const Key key{dev, M, N, K, may_split, max_floats, edges_ok};
+    const Key key{dev, M, N, K, may_split, max_floats, edges_ok, ks_ok};
     {
         std::lock_guard<std::mutex> lock(mu);
         auto it = memo.find(key);
         if (it != memo.end()) return it->second;
     }
-    const Plan p = plan_for(dev, M, N, K, may_split, max_floats, edges_ok);
+    const Plan p = plan_for(dev, M, N, K, may_split, max_floats, edges_ok, ks_ok);
     std::lock_guard<std::mutex> lock(mu);
     if (memo.size() > 4096) memo.clear();
     memo.emplace(key, p);
@@ -887,10 +997,37 @@ void run_part(const Part &p, int M, int N, int K, float alpha, const float *A, c
     }
 }
 
+// One k-sliced launch: one workgroup of KS slices per tile.
+template <class Tl, bool TA, bool TB, int EPI, int KS>
+void launch_ks(int M, int N, int K, float alpha, const float *A, const float *B, float beta,
+               float *C, const Strides &ld, bool vec, hipStream_t stream, bmb::EpiArgs ep) {
+    const int tiles_m = bmb::ceil_div(M, Tl::BM), tiles_n = bmb::ceil_div(N, Tl::BN);
+    const size_t smem = (size_t)KS * Tl::SMEM_BYTES;
+    auto go = [&](auto kern) {
+        bmb::allow_smem(kern, smem);
+        bmb::launch(kern, dim3(tiles_m * tiles_n), dim3(Tl::NT * KS), smem, stream, M, N, K,
+                    alpha, A, ld.lda, B, ld.ldb, beta, C, ld.ldc, tiles_m, tiles_n, ep);
+    };
+    if (vec) go(bf16x3_ks_k<Tl, TA, TB, true, EPI, KS>);
+    else go(bf16x3_ks_k<Tl, TA, TB, false, EPI, KS>);
+}
+
 template <bool TA, bool TB, int EPI>
 void run_band(const Part &p, int M, int N, int K, float alpha, const float *A, const float *B,
               float beta, float *C, const Strides &ld, bool vec, float *P, hipStream_t stream,
               bmb::EpiArgs ep) {
+    if (CANDS[p.tile].ks > 1) {
+        // (never planned for a split-K partial)
+        if constexpr (EPI != bmb::EPI_PARTIAL) {
+            switch (p.tile) {
+            case 4: launch_ks<TileS, TA, TB, EPI, 2>(M, N, K, alpha, A, B, beta, C, ld, vec, stream, ep); break;
+            case 5: launch_ks<TileS, TA, TB, EPI, 4>(M, N, K, alpha, A, B, beta, C, ld, vec, stream, ep); break;
+            case 6: launch_ks<TileXS, TA, TB, EPI, 4>(M, N, K, alpha, A, B, beta, C, ld, vec, stream, ep); break;
+            default: launch_ks<TileXS, TA, TB, EPI, 8>(M, N, K, alpha, A, B, beta, C, ld, vec, stream, ep); break;
+            }
+        }
+        return;
+    }
     switch (p.tile) {
     case 0: run_part<TileL, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
     case 1: run_part<TileM, TA, TB, EPI>(p, M, N, K, alpha, A, B, beta, C, ld, vec, P, stream, ep); break;
@@ -954,14 +1091,18 @@ bool bmb::bf16x3_gemm(bool ta, bool tb, int M, int N, int K, float alpha, const 
                      (((uintptr_t)B & 15) == 0);
     const bool may_split = fixed != nullptr || !bmb::stream_capturing(stream);
     const bool edges_ok = !ta && !tb && epi == bmb::EPI_BLAS;
-    Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS, edges_ok);
+    // (Every epilogue has k-sliced kernels, so a fused linear layer and
+    // gemm() plus the separate bias/GELU pass plan a shape alike and give the
+    // same bits.)
+    const bool ks_ok = true;
+    Plan p = pick(M, N, K, may_split, fixed ? fixed_floats : MAX_SPLIT_FLOATS, edges_ok, ks_ok);
     float *P = fixed;
     std::optional<bmb::ScratchLease> lease;
     const long long pf = partial_floats(p, M, N, K);
     if (pf > 0 && fixed == nullptr) {
         lease.emplace(bmb::SCRATCH_GEMM, (size_t)pf * sizeof(float), stream);
         P = static_cast<float *>(lease->get());
-        if (P == nullptr) p = pick(M, N, K, false, 0, edges_ok);  // no scratch: no split
+        if (P == nullptr) p = pick(M, N, K, false, 0, edges_ok, ks_ok);  // no scratch: no split
     }
 #define BMB_B3(TA_, TB_, EPI_)                                                              \
     run_plan<TA_, TB_, EPI_>(p, M, N, K, alpha, A, B, beta, C, vec, P, stream, ep);         \
