@@ -639,8 +639,9 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 // stages / KS) each slice runs, its stages in its own KS-th of the LDS, and
 // the slices' sums meet in LDS (Bf16x3Gemm::run). For problems with too few
 // output tiles to fill the device, where split-K would need a second launch
-// for its reduce. Interior tiles take the unguarded loop when every slice's
-// range is whole stages (K a multiple of KS * BK).
+// for its reduce. A slice of an interior tile whose range is `per` whole
+// stages takes the unguarded loop, the others the guarded one (both loops
+// pass the same number of barriers).
 template <class Tl, bool TA, bool TB, bool VEC, int EPI, int KS>
 __global__ __launch_bounds__(Tl::NT * KS) void bf16x3_ks_k(int M, int N, int K, float alpha,
                                                            const float *__restrict__ A, int lda,
@@ -660,7 +661,7 @@ __global__ __launch_bounds__(Tl::NT * KS) void bf16x3_ks_k(int M, int N, int K, 
     const float *Ak = TA ? A + (size_t)min(kb, K) * lda : A + min(kb, K);
     const float *Bk = TB ? B + min(kb, K) : B + (size_t)min(kb, K) * ldb;
     __bf16 *st = lds + (size_t)slice * 2 * Tl::STAGE;
-    if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && K > 0 && K % (KS * BK) == 0)
+    if (m0 + Tl::BM <= M && n0 + Tl::BN <= N && klen == per * BK)
         G::template run<true, EPI, false, KS>(M, N, klen, lda, ldb, alpha, Ak, Bk, beta, C, ldc,
                                               m0, n0, st, ep, per);
     else
