@@ -635,9 +635,9 @@ __global__ __launch_bounds__(Tl::NT) void bf16x3_k(int M, int N, int K, int kchu
 }
 
 // The same tile as KS k-slices of Tl::NT lanes each (any epilogue but a
-// split-K partial: it never splits): slice s takes k-stages [s per, (s + 1) per) of the per = ceil(
-// stages / KS) each slice runs, its stages in its own KS-th of the LDS, and
-// the slices' sums meet in LDS (Bf16x3Gemm::run). For problems with too few
+// split-K partial: it never splits). Every slice runs per = ceil(stages / KS)
+// stages, slice s those from s * per on, in its own KS-th of the LDS, and the
+// slices' sums meet in LDS (Bf16x3Gemm::run). For problems with too few
 // output tiles to fill the device, where split-K would need a second launch
 // for its reduce. A slice of an interior tile whose range is `per` whole
 // stages takes the unguarded loop, the others the guarded one (both loops
