@@ -24,7 +24,9 @@ The same JSON line also carries (none of them is `value`):
   * the ladder (ids 1-10) at N=4096;
   * config 3: gemm() at the GPT-2-small training shapes (BT=8192, C=768),
     forward NT, backward dX NN (beta 0) and dW TN (beta 1);
-  * config 4: flash fwd+bwd at B=8, H=12, T=1024, d=64, with its roofline;
+  * config 4: flash fwd+bwd at B=8, H=12, T=1024, d=64, with its roofline,
+    and (`flash.vs_unfused`) the unfused attention on the same inputs with
+    the fused kernels' speedup over it, as tools/test_flash.cu reports;
   * config 5: the full GPT-2-small training step (12L/768/12H, T=1024, B=8,
     V=50257 padded to 50304, fused attention, global-norm clipping, AdamW)
     on synthetic uniform tokens: tokens/s over the timed steps and the loss
@@ -1068,6 +1070,8 @@ def flash_bench(args, bmb, O, torch, traffic, V):
                      "peak_is": "fp16x3 ceiling = fp16 dense MFMA peak / 3",
                      "traffic": traffic.get("flash_fwd_bwd_b8h12t1024d64")},
     }
+    flash["vs_unfused"] = unfused_attention_bench(args, bmb, torch, d_qkv, d_dout, Bf, T, C, NH,
+                                                  f_ms, b_ms)
     if args.flash_sweep:
         sweep = {}
         for i, name in enumerate(bmb.flash_configs()):
@@ -1085,6 +1089,42 @@ def flash_bench(args, bmb, O, torch, traffic, V):
         bmb.check("flash sweep")
         flash["config_sweep_tflops"] = sweep
     return flash
+
+
+def unfused_attention_bench(args, bmb, torch, d_qkv, d_dout, Bf, T, C, NH, f_ms, b_ms):
+    """The reference's tools/test_flash.cu reports each fused path against the
+    unfused one on the same inputs (:183-192, :270-271): attention_forward
+    (3 kernels: permute, QK^T with the full T x T scores, softmax and PV,
+    unpermute) and attention_backward (7), timed here on the same q, k, v and
+    dO as the flash leg, best and median of a few launches each, and the
+    fused forward's and backward's speedup over them (the flash leg's per-step
+    times). dpreatt and datt share one buffer, as the reference's harness
+    passes them (test_flash.cu:109-110)."""
+    f32 = dict(device="cuda", dtype=torch.float32)
+    out = torch.empty(Bf * T * C, **f32)
+    qkvr = torch.empty(4 * Bf * T * C, **f32)
+    att = torch.empty(Bf * NH * T * T, **f32)
+    dqkv = torch.empty(Bf * T * 3 * C, **f32)
+    dqkvr = torch.empty(4 * Bf * T * C, **f32)
+    datt = torch.empty(Bf * NH * T * T, **f32)
+    fwd = lambda: bmb.call("attention_forward", out.data_ptr(), qkvr.data_ptr(), att.data_ptr(),
+                           d_qkv.data_ptr(), Bf, T, C, NH)
+    bwd = lambda: bmb.call("attention_backward", dqkv.data_ptr(), dqkvr.data_ptr(),
+                           datt.data_ptr(), datt.data_ptr(), d_dout.data_ptr(), qkvr.data_ptr(),
+                           att.data_ptr(), Bf, T, C, NH)
+    reps = max(3, args.steps // 4)
+    fs = stats(timed(fwd, reps, 2, "unfused attention fwd"))
+    bs = stats(timed(bwd, reps, 2, "unfused attention bwd"))
+    bmb.check("unfused attention")
+    res = {"fwd_best_ms": round(fs["best_ms"], 4), "fwd_median_ms": round(fs["median_ms"], 4),
+           "bwd_best_ms": round(bs["best_ms"], 4), "bwd_median_ms": round(bs["median_ms"], 4),
+           "fused_fwd_speedup": round(fs["median_ms"] / f_ms, 2),
+           "fused_bwd_speedup": round(bs["median_ms"] / b_ms, 2),
+           "note": "this build's unfused attention (attention.h: fp32 MFMA batched GEMMs and the "
+                   "materialised causal softmax) against its default flash kernels"}
+    del out, qkvr, att, dqkv, dqkvr, datt
+    torch.cuda.empty_cache()
+    return res
 
 
 if __name__ == "__main__":
