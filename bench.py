@@ -94,7 +94,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline SGEMM and flash only")
     ap.add_argument("--only", choices=["sgemm", "flash", "gpt", "sizes"], default=None,
                     help="run one workload only (for profiling); sizes: KERNELS ids 8, 9 "
-                         "and 10 at N = 512, 1024 and 4096")
+                         "and 10 at N = 512, 1024, 4096 and 4097")
     ap.add_argument("--flash-sweep", action="store_true",
                     help="also time every forward and backward flash config (as the "
                          "reference's tools/test_flash.cu:198-227,279-319 sweep does)")
