@@ -635,3 +635,47 @@ def test_k_sliced_tiles(gpu, shape, trans, capfd, monkeypatch):
     assert bad == 0 and err < 1e-4, err
     e3, bound = bf16x3_err(got, ta, tb, M, N, K, 0.75, A, B, 1.25, C0)
     assert e3 < bound, (e3, bound)
+
+
+# Shapes drawn at random (fixed seed), run through whatever plan each planner
+# picks for them -- whole tiles, k-sliced workgroups, split-K, row bands,
+# corner plans -- in both arithmetic modes and all four transposes. C sits
+# between canary bands (no write outside it); sampled rows of op(A) against
+# fp64: the reference's 1e-4, and each mode's own bound.
+def _random_shapes(n, seed):
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 2600)), int(r.integers(1, 2600)), int(r.integers(1, 5000)))
+            for _ in range(n)]
+
+
+RANDOM_SHAPES = _random_shapes(12, 2024)
+
+
+@pytest.mark.parametrize("math", [0, 1], ids=["bf16x3", "fp32"])
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("shape", RANDOM_SHAPES, ids=lambda s: "%dx%dx%d" % s)
+def test_random_shapes(gpu, shape, trans, math):
+    M, N, K = shape
+    ta, tb = trans
+    A = O.fill_xorshift(M * K, 0x3131 + M)
+    B = O.fill_xorshift(K * N, 0x4141 + N)
+    C0 = O.fill_xorshift(M * N, 0x5151 + K)
+    with bmb.gemm_math(math):
+        dA, dB = dev(A), dev(B)
+        gC = Guarded(M * N, fill=C0)
+        print("gemm %s %dx%dx%d math %d" % (_tag(trans), M, N, K, math), flush=True)
+        bmb.gemm(ta, tb, M, N, K, 0.75, dA.data_ptr(), dB.data_ptr(), 1.25, gC.ptr)
+        sync("gemm random shape")
+    assert gC.ok()
+    rows = np.unique(np.r_[0, M // 2, M - 1, np.random.default_rng(M + N + K).integers(0, M, 9)])
+    Aop = np.ascontiguousarray((A.reshape(K, M).T if ta else A.reshape(M, K))[rows])
+    c0 = np.ascontiguousarray(C0.reshape(M, N)[rows])
+    got = gC.get().reshape(M, N)[rows]
+    ref = O.gemm_f64(False, tb, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+    err, bad = O.normwise(got, ref)
+    assert bad == 0 and err < 1e-4, err
+    if math == 0:
+        e3, bound = bf16x3_err(got, False, tb, len(rows), N, K, 0.75, Aop, B, 1.25, c0)
+        assert e3 < bound, (e3, bound)
+    else:
+        assert err < fp32_order_bound(K), (err, fp32_order_bound(K))
