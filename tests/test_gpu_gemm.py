@@ -679,3 +679,33 @@ def test_random_shapes(gpu, shape, trans, math):
         assert e3 < bound, (e3, bound)
     else:
         assert err < fp32_order_bound(K), (err, fp32_order_bound(K))
+
+
+def _random_batched(n, seed):
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 9)), int(r.integers(1, 400)), int(r.integers(1, 400)),
+             int(r.integers(1, 3000))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("trans", TRANS, ids=_tag)
+@pytest.mark.parametrize("bshape", _random_batched(8, 77), ids=lambda s: "b%d_%dx%dx%d" % s)
+def test_random_batched(gpu, bshape, trans):
+    """batched_gemm() on random shapes (fixed seed): whole-K tiles or
+    k-sliced workgroups, whatever its planner picks; every problem of the
+    batch within fp32_order_bound(K) of fp64, C between canary bands."""
+    batch, M, N, K = bshape
+    ta, tb = trans
+    eA, eB, eC = M * K, K * N, M * N
+    A = O.fill_xorshift(eA * batch, 0x6262 + K)
+    B = O.fill_xorshift(eB * batch, 0x7272 + M)
+    C0 = O.fill_xorshift(eC * batch, 0x8282 + N)
+    dA, dB = dev(A), dev(B)
+    gC = Guarded(eC * batch, fill=C0)
+    print("batched %s batch=%d M=%d N=%d K=%d" % (_tag(trans), batch, M, N, K), flush=True)
+    bmb.batched_gemm(ta, tb, batch, M, N, K, 0.5, dA.data_ptr(), eA, dB.data_ptr(), eB,
+                     2.0, gC.ptr, eC)
+    sync("batched_gemm random")
+    assert gC.ok()
+    ref = O.batched_gemm_f64(ta, tb, batch, M, N, K, 0.5, A, eA, B, eB, 2.0, C0, eC)
+    err, bad = O.normwise(gC.get(), ref)
+    assert bad == 0 and err < fp32_order_bound(K), (err, fp32_order_bound(K))
