@@ -144,6 +144,23 @@ def test_ragged_shapes(gpu, shape):
     _case(*shape, 4321, 8765)
 
 
+def _random_flash_shapes(n, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        hs = int(r.choice([32, 64, 128]))
+        NH = int(r.integers(1, 9))
+        out.append((int(r.integers(1, 5)), int(r.integers(1, 900)), hs * NH, NH))
+    return out
+
+
+@pytest.mark.parametrize("shape", _random_flash_shapes(6, 99), ids=lambda s: "B%dT%dC%dNH%d" % s)
+def test_random_shapes(gpu, shape):
+    """Default configs on random (B, T, head size, heads), fixed seed: the same
+    1e-5 and derived bars against fp64 as every other case."""
+    _case(*shape, 2468, 1357)
+
+
 MAX_CFGS = 10  # more than either table holds; ids past the end are skipped
 
 
