@@ -26,7 +26,7 @@ TOL = 1e-5
 NTHREADS = 4
 
 
-def _work(qkv, dout, A, B, C0, shape, gshape, results, errors, i, barrier):
+def _worker(qkv, dout, A, B, C0, shape, gshape, results, errors, i, barrier):
     import torch
     try:
         Bn, T, C, NH = shape
@@ -61,7 +61,7 @@ def test_concurrent_host_threads(gpu):
     C0 = O.fill_xorshift(M * N, 0x9999)
     results, errors = [None] * NTHREADS, []
     barrier = threading.Barrier(NTHREADS)
-    threads = [threading.Thread(target=_work, args=(qkv, dout, A, B, C0, shape, gshape, results,
+    threads = [threading.Thread(target=_worker, args=(qkv, dout, A, B, C0, shape, gshape, results,
                                                     errors, i, barrier))
                for i in range(NTHREADS)]
     print("threads: %d x (flash fwd+bwd B=%d T=%d C=%d NH=%d, gemm %dx%dx%d)"
